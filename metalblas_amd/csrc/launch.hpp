@@ -1,0 +1,102 @@
+// Internal launcher interface between the C ABI / planner (mb_api.hip) and the kernel
+// translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mb_types.hpp"
+
+namespace mb {
+
+// dtype codes (same values as mb_dtype in include/metalblas_amd.h)
+enum Dt : int { F32 = 0, F16, BF16, C64, C32, I8, U8, I16, I32, I64, DT_COUNT };
+
+inline int dtype_size(int dt) {
+    switch (dt) {
+        case F32: return 4;
+        case F16: case BF16: return 2;
+        case C64: return 8;
+        case C32: return 4;
+        case I8: case U8: return 1;
+        case I16: return 2;
+        case I32: return 4;
+        case I64: return 8;
+    }
+    return 0;
+}
+// bytes of one accumulator element (split-K partial planes)
+inline int acc_size(int dt) {
+    switch (dt) {
+        case C64: case C32: case I64: return 8;
+        default: return 4;
+    }
+}
+
+// Invoke f.template operator()<T>() with the storage type of dtype `dt`.
+template <class F> inline hipError_t with_dtype(int dt, F &&f) {
+    switch (dt) {
+        case F32: return f.template operator()<float>();
+        case F16: return f.template operator()<f16_t>();
+        case BF16: return f.template operator()<bf16_t>();
+        case C64: return f.template operator()<c64_t>();
+        case C32: return f.template operator()<c32_t>();
+        case I8: return f.template operator()<int8_t>();
+        case U8: return f.template operator()<uint8_t>();
+        case I16: return f.template operator()<int16_t>();
+        case I32: return f.template operator()<int32_t>();
+        case I64: return f.template operator()<int64_t>();
+    }
+    return hipErrorInvalidValue;
+}
+
+// ---- GEMV families --------------------------------------------------------------------
+// Y(i, v) = sum_k Mat(i, k) * X(k, v)   for i < rows, v < nv   (one problem per batch index)
+//   dot  family: Mat(i, k) at mat[i*mat_ld + k]     (rows contiguous along K)
+//   axpy family: Mat(i, k) at mat[k*mat_ld + i]     (rows of the stored matrix run along i)
+struct GemvArgs {
+    const void *mat;
+    int64_t mat_ld, mat_bs;
+    const void *x;
+    int64_t x_ks, x_vs, x_bs;
+    void *y;
+    int64_t y_is, y_vs, y_bs;
+    const void *bias;
+    int64_t bias_is, bias_vs, bias_bs;
+    void *ws;   // axpy split partials: acc-typed [splits][batch][nv][rows]
+    int32_t rows, K, nv, batch;
+    int32_t conj_mat, conj_x;
+    int32_t epilogue, beta_nz, alpha_nz;
+    int32_t vec_ok;
+    int32_t splits, k_chunk;
+    EpiScalars s;
+};
+
+struct LaunchShape {
+    dim3 grid, block;
+};
+
+// gemm_generic.hip
+hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
+hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);
+hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st);
+
+// gemv.hip
+int gemv_nv_bucket(int nv);   // template NV used for a given number of vectors
+hipError_t launch_gemv_dot(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
+hipError_t launch_gemv_axpy(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
+int gemv_axpy_vec(int dt, int nv);   // elements per lane of the vector path
+
+// gemm_mfma.hip
+struct MfmaTile {
+    int bm, bn, wm, wn;   // block tile and wave grid
+};
+bool mfma_supported_dtype(int dt);
+int mfma_k_align(int dt);   // elements per 16-byte chunk along K
+bool mfma_tile_compiled(int dt, const MfmaTile &t);
+int mfma_list_tiles(int dt, MfmaTile *out, int cap);
+// a_kc: A contiguous along K (row-major A);  b_kc: B contiguous along K (column-major B)
+hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g,
+                       hipStream_t st, LaunchShape *shape);
+
+}  // namespace mb

@@ -1,0 +1,609 @@
+// C ABI and planner of libmetalblas_hip.so.
+//
+// The planner restates the decisions of the reference's L3 planners for gfx950
+// (metalblas/float_dispatch.py:745-852 backend choice, :484-505 plan cache, :613-655 tile
+// picker, :210-219 split-K regime; metalblas/integer_dispatch.py:92-117;
+// metalblas/complex_dispatch.py:33-66 GEMV routing) and re-derives the numbers for 256 CUs
+// and 160 KB of LDS: thin products (M or N <= 16) stream the matrix once through the GEMV
+// families, aligned bf16/fp16/fp32/int8/uint8 products run on the matrix-core family, and
+// everything else on the generic tiled kernel.
+#include <cmath>
+#include <mutex>
+#include <utility>
+#include <string.h>
+
+#include "../../include/metalblas_amd.h"
+#include "launch.hpp"
+
+using namespace mb;
+
+namespace {
+
+constexpr int64_t kI32Max = 2147483647;
+
+struct Operand {
+    const char *ptr;
+    int64_t rs, cs, bs;
+};
+
+// Normalised problem (element strides, int64 sizes), possibly transposed.
+struct Prob {
+    int dt;
+    int64_t batch, M, N, K;
+    Operand a, b, c, bias;
+    int conj_a, conj_b;
+    int epilogue, beta_nz, alpha_nz;
+    EpiScalars s;
+    int backend;
+    int32_t tile[8];
+    int swz;
+    int split_req;
+    bool transposed;
+};
+
+struct Plan {
+    int family = MB_FAMILY_NONE;
+    Prob p;
+    // GEMV
+    GemvArgs gv;
+    bool gemv_dot = false;
+    // MFMA / generic
+    GemmArgs gg;
+    MfmaTile tile = {0, 0, 0, 0};
+    bool a_kc = false, b_kc = false;
+    int64_t ws_bytes = 0;
+};
+
+struct DevInfo {
+    bool init = false;
+    int cus = 256;
+    int arch = 0;
+    int64_t lds = 65536;
+};
+std::mutex g_dev_mu;
+DevInfo g_dev[64];
+
+const DevInfo &dev_info() {
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= 64) d = 0;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    DevInfo &di = g_dev[d];
+    if (!di.init) {
+        hipDeviceProp_t pr;
+        if (hipGetDeviceProperties(&pr, d) == hipSuccess) {
+            di.cus = pr.multiProcessorCount > 0 ? pr.multiProcessorCount : 256;
+            di.lds = (int64_t)pr.sharedMemPerBlock;
+            const char *n = pr.gcnArchName;
+            if (strncmp(n, "gfx", 3) == 0) {
+                int v = 0;
+                for (const char *q = n + 3; *q >= '0' && *q <= '9'; ++q) v = v * 10 + (*q - '0');
+                di.arch = v;
+            }
+        }
+        di.init = true;
+    }
+    return di;
+}
+
+bool aligned(const void *p, int bytes) { return ((uintptr_t)p % (uintptr_t)bytes) == 0; }
+int ilog2_floor(int64_t v) {
+    int r = 0;
+    while ((int64_t(1) << (r + 1)) <= v) ++r;
+    return r;
+}
+
+int normalise(const mb_gemm_desc *d, Prob &p) {
+    if (!d) return MB_ERR_INVALID_ARG;
+    if (d->dtype < 0 || d->dtype >= MB_DTYPE_COUNT) return MB_ERR_UNSUPPORTED_DTYPE;
+    if (d->backend < 0 || d->backend >= MB_BACKEND_COUNT) return MB_ERR_BAD_BACKEND;
+    if (d->batch < 0 || d->M < 0 || d->N < 0 || d->K < 0) return MB_ERR_INVALID_ARG;
+    if (d->batch > kI32Max || d->M > kI32Max || d->N > kI32Max || d->K > kI32Max) return MB_ERR_INVALID_ARG;
+    if (d->flags != 0) return MB_ERR_INVALID_ARG;
+    p.dt = d->dtype;
+    p.batch = d->batch;
+    p.M = d->M;
+    p.N = d->N;
+    p.K = d->K;
+    p.a = {(const char *)d->a.ptr, d->a.row_stride, d->a.col_stride, d->a.batch_stride};
+    p.b = {(const char *)d->b.ptr, d->b.row_stride, d->b.col_stride, d->b.batch_stride};
+    p.c = {(const char *)d->c.ptr, d->c.row_stride, d->c.col_stride, d->c.batch_stride};
+    p.bias = {(const char *)d->bias.ptr, d->bias.row_stride, d->bias.col_stride, d->bias.batch_stride};
+    const bool cplx = p.dt == MB_DTYPE_C64 || p.dt == MB_DTYPE_C32;
+    p.conj_a = cplx && d->conj_a;
+    p.conj_b = cplx && d->conj_b;
+    p.epilogue = d->epilogue != 0;
+    p.beta_nz = p.epilogue && d->beta_nz;
+    p.alpha_nz = p.epilogue ? (d->alpha_nz != 0) : 1;
+    p.s.alpha_re = (float)d->alpha_re;
+    p.s.alpha_im = (float)d->alpha_im;
+    p.s.beta_re = (float)d->beta_re;
+    p.s.beta_im = (float)d->beta_im;
+    p.s.alpha_u = (uint64_t)d->alpha_int;
+    p.s.beta_u = (uint64_t)d->beta_int;
+    p.backend = d->backend;
+    memcpy(p.tile, d->tile, sizeof(p.tile));
+    p.swz = d->swizzle_log;
+    p.split_req = d->split_k;
+    p.transposed = false;
+    if (p.batch == 0 || p.M == 0 || p.N == 0) return MB_OK;
+    if (!p.c.ptr) return MB_ERR_INVALID_ARG;
+    if (p.K > 0 && (!p.a.ptr || !p.b.ptr)) return MB_ERR_INVALID_ARG;
+    if (p.beta_nz && !p.bias.ptr) return MB_ERR_INVALID_ARG;
+    if (p.backend == MB_BACKEND_GEMV && p.M != 1 && p.N != 1) return MB_ERR_GEMV_SHAPE;
+    return MB_OK;
+}
+
+// C^T = B^T A^T: swap operands and their row/col strides.
+void transpose(Prob &p) {
+    std::swap(p.M, p.N);
+    Operand a = p.a, b = p.b;
+    p.a = {b.ptr, b.cs, b.rs, b.bs};
+    p.b = {a.ptr, a.cs, a.rs, a.bs};
+    p.c = {p.c.ptr, p.c.cs, p.c.rs, p.c.bs};
+    p.bias = {p.bias.ptr, p.bias.cs, p.bias.rs, p.bias.bs};
+    std::swap(p.conj_a, p.conj_b);
+    p.transposed = !p.transposed;
+}
+
+void fill_gemm_args(const Prob &p, GemmArgs &g) {
+    memset(&g, 0, sizeof(g));
+    g.a = p.a.ptr;
+    g.b = p.b.ptr;
+    g.c = (void *)p.c.ptr;
+    g.bias = p.bias.ptr;
+    g.a_rs = p.a.rs; g.a_cs = p.a.cs; g.a_bs = p.a.bs;
+    g.b_rs = p.b.rs; g.b_cs = p.b.cs; g.b_bs = p.b.bs;
+    g.c_rs = p.c.rs; g.c_cs = p.c.cs; g.c_bs = p.c.bs;
+    g.bias_rs = p.bias.rs; g.bias_cs = p.bias.cs; g.bias_bs = p.bias.bs;
+    g.M = (int)p.M; g.N = (int)p.N; g.K = (int)p.K; g.batch = (int)p.batch;
+    g.conj_a = p.conj_a; g.conj_b = p.conj_b;
+    g.epilogue = p.epilogue; g.beta_nz = p.beta_nz; g.alpha_nz = p.alpha_nz;
+    g.splits = 1;
+    g.k_chunk = (int)(p.K > 0 ? p.K : 1);
+    g.swz = 0;
+    g.s = p.s;
+}
+
+// ---- GEMV planning ----------------------------------------------------------------------
+// Returns true and fills the plan when the thin side can be streamed by a GEMV family.
+bool plan_gemv(const Prob &p, Plan &pl) {
+    const int es = dtype_size(p.dt);
+    const bool n_thin = p.N <= p.M;   // thin output dimension: N (matrix = A) or M (matrix = B)
+    const int64_t nv = n_thin ? p.N : p.M;
+    if (nv > 16) return false;
+    GemvArgs g;
+    memset(&g, 0, sizeof(g));
+    bool dot;
+    if (n_thin) {
+        if (p.a.cs == 1) {
+            dot = true;
+            g.mat = p.a.ptr; g.mat_ld = p.a.rs;
+        } else if (p.a.rs == 1) {
+            dot = false;
+            g.mat = p.a.ptr; g.mat_ld = p.a.cs;
+        } else {
+            return false;
+        }
+        g.mat_bs = p.a.bs;
+        g.x = p.b.ptr; g.x_ks = p.b.rs; g.x_vs = p.b.cs; g.x_bs = p.b.bs;
+        g.y = (void *)p.c.ptr; g.y_is = p.c.rs; g.y_vs = p.c.cs; g.y_bs = p.c.bs;
+        g.bias = p.bias.ptr; g.bias_is = p.bias.rs; g.bias_vs = p.bias.cs; g.bias_bs = p.bias.bs;
+        g.conj_mat = p.conj_a; g.conj_x = p.conj_b;
+        g.rows = (int)p.M;
+    } else {
+        if (p.b.cs == 1) {
+            dot = false;
+            g.mat = p.b.ptr; g.mat_ld = p.b.rs;
+        } else if (p.b.rs == 1) {
+            dot = true;
+            g.mat = p.b.ptr; g.mat_ld = p.b.cs;
+        } else {
+            return false;
+        }
+        g.mat_bs = p.b.bs;
+        g.x = p.a.ptr; g.x_ks = p.a.cs; g.x_vs = p.a.rs; g.x_bs = p.a.bs;
+        g.y = (void *)p.c.ptr; g.y_is = p.c.cs; g.y_vs = p.c.rs; g.y_bs = p.c.bs;
+        g.bias = p.bias.ptr; g.bias_is = p.bias.cs; g.bias_vs = p.bias.rs; g.bias_bs = p.bias.bs;
+        g.conj_mat = p.conj_b; g.conj_x = p.conj_a;
+        g.rows = (int)p.N;
+    }
+    g.K = (int)p.K;
+    g.nv = (int)nv;
+    g.batch = (int)p.batch;
+    g.epilogue = p.epilogue; g.beta_nz = p.beta_nz; g.alpha_nz = p.alpha_nz;
+    g.s = p.s;
+    g.splits = 1;
+    g.k_chunk = g.K;
+    const bool batched = p.batch > 1;
+    if (dot) {
+        const int V = 16 / es;
+        bool ok = aligned(g.mat, 16) && (g.mat_ld * es) % 16 == 0 && (!batched || (g.mat_bs * es) % 16 == 0);
+        ok = ok && (g.K % V) == 0 && g.x_ks == 1 && aligned(g.x, 16) && (!batched || (g.x_bs * es) % 16 == 0);
+        ok = ok && (nv == 1 || (g.x_vs * es) % 16 == 0);
+        g.vec_ok = ok;
+    } else {
+        const int V = gemv_axpy_vec(p.dt, (int)nv);
+        const int vb = V * es;
+        bool ok = aligned(g.mat, vb) && (g.mat_ld * es) % vb == 0 && (!batched || (g.mat_bs * es) % vb == 0);
+        ok = ok && (g.rows % V) == 0;
+        g.vec_ok = ok;
+        const int vv = ok ? V : 1;
+        const int64_t waves = ((int64_t)g.rows + 64 * vv - 1) / (64 * vv) * p.batch;
+        const int cus = dev_info().cus;
+        int64_t splits = (8LL * cus + waves - 1) / waves;
+        const int64_t max_splits = (p.K + 63) / 64;
+        if (splits > max_splits) splits = max_splits;
+        if (splits > 256) splits = 256;
+        if (splits < 1) splits = 1;
+        if (splits > 1) {
+            int64_t chunk = (p.K + splits - 1) / splits;
+            chunk = (chunk + 7) / 8 * 8;
+            splits = (p.K + chunk - 1) / chunk;
+            g.k_chunk = (int)chunk;
+            g.splits = (int)splits;
+            pl.ws_bytes = splits * p.batch * nv * (int64_t)g.rows * acc_size(p.dt);
+        }
+    }
+    pl.family = dot ? MB_FAMILY_GEMV_DOT : MB_FAMILY_GEMV_AXPY;
+    pl.gemv_dot = dot;
+    pl.gv = g;
+    return true;
+}
+
+// ---- matrix-core planning ---------------------------------------------------------------
+MfmaTile snap_tile(int dt, const int32_t *t, int backend) {
+    MfmaTile want = {t[0], t[1], 2, 2};
+    if (backend == MB_BACKEND_TILED && t[3] > 0 && t[4] > 0) {
+        want.wm = t[3];
+        want.wn = t[4];
+    }
+    MfmaTile list[32];
+    const int n = mfma_list_tiles(dt, list, 32);
+    int best = 0;
+    double bestd = 1e30;
+    for (int i = 0; i < n && i < 32; ++i) {
+        double d = fabs(log2((double)list[i].bm / (want.bm > 0 ? want.bm : 1))) +
+                   fabs(log2((double)list[i].bn / (want.bn > 0 ? want.bn : 1)));
+        if (list[i].wm != want.wm || list[i].wn != want.wn) d += 0.01;
+        if (d < bestd) {
+            bestd = d;
+            best = i;
+        }
+    }
+    return list[best];
+}
+
+bool mfma_layout_ok(const Prob &p, bool &a_kc, bool &b_kc) {
+    if (!mfma_supported_dtype(p.dt)) return false;
+    const int es = dtype_size(p.dt);
+    const int E = 16 / es;
+    const bool batched = p.batch > 1;
+    // A
+    if (p.a.cs == 1) {
+        a_kc = true;
+        if ((p.a.rs * es) % 16 || p.K % E) return false;
+    } else if (p.a.rs == 1) {
+        a_kc = false;
+        if ((p.a.cs * es) % 16 || p.M % E) return false;
+    } else {
+        return false;
+    }
+    if (!aligned(p.a.ptr, 16) || (batched && (p.a.bs * es) % 16)) return false;
+    // B
+    if (p.b.rs == 1) {
+        b_kc = true;
+        if ((p.b.cs * es) % 16 || p.K % E) return false;
+    } else if (p.b.cs == 1) {
+        b_kc = false;
+        if ((p.b.rs * es) % 16 || p.N % E) return false;
+    } else {
+        return false;
+    }
+    if (!aligned(p.b.ptr, 16) || (batched && (p.b.bs * es) % 16)) return false;
+    return true;
+}
+
+void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
+    const int cus = dev_info().cus;
+    MfmaTile t;
+    const bool forced = (p.backend == MB_BACKEND_MATRIX || p.backend == MB_BACKEND_TILED) && p.tile[0] > 0 &&
+                        p.tile[1] > 0;
+    if (forced) {
+        t = snap_tile(p.dt, p.tile, p.backend);
+    } else {
+        static const MfmaTile order[] = {{256, 256, 2, 2}, {256, 128, 2, 2}, {128, 256, 2, 2},
+                                         {128, 128, 2, 2}, {128, 64, 2, 2},  {64, 128, 2, 2},
+                                         {64, 64, 2, 2}};
+        t = {32, 32, 1, 1};
+        for (const auto &o : order) {
+            const int64_t tiles = ((p.M + o.bm - 1) / o.bm) * ((p.N + o.bn - 1) / o.bn) * p.batch;
+            if (tiles >= cus) {
+                t = o;
+                break;
+            }
+        }
+        if (t.bm == 32) {
+            // too few tiles for the big shapes: smallest 4-wave tile unless the problem is tiny
+            const int64_t t64 = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.batch;
+            if (t64 >= 16 || p.K >= 1024) t = {64, 64, 2, 2};
+        }
+    }
+    GemmArgs &g = pl.gg;
+    fill_gemm_args(p, g);
+    const int es = dtype_size(p.dt);
+    const int BK = 8 * (16 / es);
+    const int64_t tiles = ((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * p.batch;
+    int64_t splits = 1;
+    if (p.split_req > 1) {
+        splits = p.split_req;
+    } else if (p.split_req == 0 && p.backend == MB_BACKEND_AUTO && tiles < cus && p.K >= 2048) {
+        splits = (2LL * cus + tiles - 1) / tiles;
+        const int64_t maxs = p.K / (4 * BK);
+        if (splits > maxs) splits = maxs;
+        if (splits > 64) splits = 64;
+        if (splits < 1) splits = 1;
+    }
+    if (splits > 1) {
+        int64_t chunk = (p.K + splits - 1) / splits;
+        chunk = (chunk + BK - 1) / BK * BK;
+        splits = (p.K + chunk - 1) / chunk;
+        g.k_chunk = (int)chunk;
+    }
+    g.splits = (int)splits;
+    if (splits > 1) pl.ws_bytes = splits * p.batch * p.M * p.N * acc_size(p.dt);
+    const int64_t tiles_m = (p.M + t.bm - 1) / t.bm;
+    int swz = p.swz;
+    if (swz < 0) swz = tiles_m >= 8 ? 3 : ilog2_floor(tiles_m > 0 ? tiles_m : 1);
+    if (swz > 6) swz = 6;
+    g.swz = swz;
+    // vector stores: C row-major, 4-element groups aligned
+    g.vec_ok = p.c.cs == 1 && (p.c.rs % 4) == 0 && aligned(p.c.ptr, 4 * es) &&
+               (p.batch == 1 || (p.c.bs % 4) == 0);
+    pl.family = MB_FAMILY_MFMA;
+    pl.tile = t;
+    pl.a_kc = a_kc;
+    pl.b_kc = b_kc;
+}
+
+void plan_generic(const Prob &p, Plan &pl) {
+    GemmArgs &g = pl.gg;
+    fill_gemm_args(p, g);
+    const int cus = dev_info().cus;
+    const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.batch;
+    int64_t splits = 1;
+    if (p.split_req > 1) {
+        splits = p.split_req;
+    } else if (p.split_req == 0 && tiles < cus && p.K >= 1024) {
+        splits = (2LL * cus + tiles - 1) / tiles;
+        const int64_t maxs = p.K / 256;
+        if (splits > maxs) splits = maxs;
+        if (splits > 64) splits = 64;
+        if (splits < 1) splits = 1;
+    }
+    if (splits > 1) {
+        int64_t chunk = (p.K + splits - 1) / splits;
+        chunk = (chunk + 15) / 16 * 16;
+        splits = (p.K + chunk - 1) / chunk;
+        g.k_chunk = (int)chunk;
+        pl.ws_bytes = splits * p.batch * p.M * p.N * acc_size(p.dt);
+    }
+    g.splits = (int)splits;
+    pl.family = MB_FAMILY_GENERIC;
+}
+
+int make_plan(const mb_gemm_desc *d, Plan &pl) {
+    Prob p;
+    int st = normalise(d, p);
+    if (st != MB_OK) return st;
+    pl.family = MB_FAMILY_NONE;
+    pl.ws_bytes = 0;
+    if (p.batch == 0 || p.M == 0 || p.N == 0) {
+        pl.p = p;
+        return MB_OK;
+    }
+    if (p.K == 0) {
+        pl.p = p;
+        fill_gemm_args(p, pl.gg);
+        pl.family = MB_FAMILY_FILL;
+        return MB_OK;
+    }
+    // column-major outputs are produced as the transposed row-major problem
+    if (p.c.cs != 1 && p.c.rs == 1) transpose(p);
+    pl.p = p;
+
+    if (p.backend == MB_BACKEND_GENERIC) {
+        plan_generic(p, pl);
+        return MB_OK;
+    }
+    const bool thin = p.M <= 16 || p.N <= 16;
+    if (p.backend == MB_BACKEND_GEMV || (p.backend == MB_BACKEND_AUTO && thin)) {
+        if (plan_gemv(p, pl)) return MB_OK;
+        if (p.backend == MB_BACKEND_GEMV) {
+            // a gemv request whose matrix has no unit stride: generic kernel, same results
+            plan_generic(p, pl);
+            return MB_OK;
+        }
+    }
+    bool a_kc = false, b_kc = false;
+    if (mfma_layout_ok(p, a_kc, b_kc) && !(p.backend == MB_BACKEND_AUTO && p.M < 32 && p.N < 32)) {
+        plan_mfma(p, pl, a_kc, b_kc);
+        return MB_OK;
+    }
+    plan_generic(p, pl);
+    return MB_OK;
+}
+
+int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape) {
+    hipError_t e = hipSuccess;
+    // workspace: fall back to a single K slice when the caller gave too little
+    if (pl.ws_bytes > 0 && (!d->workspace || d->workspace_bytes < pl.ws_bytes)) return MB_ERR_WORKSPACE;
+    switch (pl.family) {
+        case MB_FAMILY_NONE:
+            return MB_OK;
+        case MB_FAMILY_FILL:
+            e = launch_fill(pl.p.dt, pl.gg, st);
+            break;
+        case MB_FAMILY_GENERIC:
+        case MB_FAMILY_MFMA: {
+            GemmArgs &g = pl.gg;
+            g.ws = d->workspace;
+            e = pl.family == MB_FAMILY_MFMA ? launch_mfma(pl.p.dt, pl.tile, pl.a_kc, pl.b_kc, g, st, shape)
+                                            : launch_generic(pl.p.dt, g, st, shape);
+            if (e == hipSuccess && g.splits > 1) e = launch_splitk_reduce(pl.p.dt, g, st);
+            break;
+        }
+        case MB_FAMILY_GEMV_DOT:
+            e = launch_gemv_dot(pl.p.dt, pl.gv, st, shape);
+            break;
+        case MB_FAMILY_GEMV_AXPY: {
+            GemvArgs &g = pl.gv;
+            g.ws = d->workspace;
+            e = launch_gemv_axpy(pl.p.dt, g, st, shape);
+            if (e == hipSuccess && g.splits > 1) {
+                // sum the K slices: partial planes are [split][batch][nv][rows]
+                GemmArgs r;
+                memset(&r, 0, sizeof(r));
+                r.ws = g.ws;
+                r.c = g.y;
+                r.bias = g.bias;
+                r.M = g.nv; r.N = g.rows; r.batch = g.batch;
+                r.c_rs = g.y_vs; r.c_cs = g.y_is; r.c_bs = g.y_bs;
+                r.bias_rs = g.bias_vs; r.bias_cs = g.bias_is; r.bias_bs = g.bias_bs;
+                r.epilogue = g.epilogue; r.beta_nz = g.beta_nz; r.alpha_nz = g.alpha_nz;
+                r.s = g.s;
+                r.splits = g.splits;
+                e = launch_splitk_reduce(pl.p.dt, r, st);
+            }
+            break;
+        }
+        default:
+            return MB_ERR_INVALID_ARG;
+    }
+    return e == hipSuccess ? MB_OK : MB_ERR_LAUNCH;
+}
+
+// Drop split-K when no workspace was provided (correct results, less parallelism).
+void drop_split_without_ws(Plan &pl, const mb_gemm_desc *d) {
+    if (pl.ws_bytes <= 0) return;
+    if (d->workspace && d->workspace_bytes >= pl.ws_bytes) return;
+    pl.ws_bytes = 0;
+    if (pl.family == MB_FAMILY_GEMV_AXPY) {
+        pl.gv.splits = 1;
+        pl.gv.k_chunk = pl.gv.K;
+    } else {
+        pl.gg.splits = 1;
+        pl.gg.k_chunk = pl.gg.K;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int mb_gemm(const mb_gemm_desc *desc, void *stream) {
+    Plan pl;
+    int st = make_plan(desc, pl);
+    if (st != MB_OK) return st;
+    drop_split_without_ws(pl, desc);
+    return run_plan(pl, desc, (hipStream_t)stream, nullptr);
+}
+
+int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
+    Plan pl;
+    int st = make_plan(desc, pl);
+    if (st != MB_OK) return st;
+    return pl.ws_bytes;
+}
+
+int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
+    if (!info) return MB_ERR_INVALID_ARG;
+    Plan pl;
+    int st = make_plan(desc, pl);
+    if (st != MB_OK) return st;
+    memset(info, 0, sizeof(*info));
+    info->family = pl.family;
+    info->transposed = pl.p.transposed;
+    info->workspace_bytes = pl.ws_bytes;
+    info->split_k = 1;
+    if (pl.family == MB_FAMILY_MFMA) {
+        info->tile[0] = pl.tile.bm;
+        info->tile[1] = pl.tile.bn;
+        info->tile[2] = 8 * (16 / dtype_size(pl.p.dt));
+        info->tile[3] = pl.tile.wm;
+        info->tile[4] = pl.tile.wn;
+        info->tile[5] = pl.a_kc;
+        info->tile[6] = pl.b_kc;
+        info->split_k = pl.gg.splits;
+        info->swizzle_log = pl.gg.swz;
+        info->block = 64 * pl.tile.wm * pl.tile.wn;
+        info->grid[0] = (int)(((pl.p.M + pl.tile.bm - 1) / pl.tile.bm) * ((pl.p.N + pl.tile.bn - 1) / pl.tile.bn));
+        info->grid[1] = pl.gg.splits;
+        info->grid[2] = (int)(pl.p.batch < 65535 ? pl.p.batch : 65535);
+    } else if (pl.family == MB_FAMILY_GENERIC) {
+        info->tile[0] = 64;
+        info->tile[1] = 64;
+        info->tile[2] = 16;
+        info->split_k = pl.gg.splits;
+        info->block = 256;
+    } else if (pl.family == MB_FAMILY_GEMV_DOT || pl.family == MB_FAMILY_GEMV_AXPY) {
+        info->tile[0] = pl.gv.nv;
+        info->tile[1] = pl.gv.vec_ok;
+        info->split_k = pl.gv.splits;
+        info->block = 256;
+    }
+    return MB_OK;
+}
+
+int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
+    Plan pl;
+    int st = make_plan(desc, pl);
+    if (st != MB_OK) return st;
+    if (pl.family != MB_FAMILY_MFMA) return 0;
+    MfmaTile list[32];
+    const int n = mfma_list_tiles(pl.p.dt, list, 32);
+    int out = 0;
+    auto emit = [&](const MfmaTile &t) {
+        if (out < cap && tiles) {
+            int32_t *q = tiles + 8 * out;
+            memset(q, 0, 8 * sizeof(int32_t));
+            q[0] = t.bm; q[1] = t.bn; q[2] = 8 * (16 / dtype_size(pl.p.dt)); q[3] = t.wm; q[4] = t.wn;
+        }
+        ++out;
+    };
+    emit(pl.tile);
+    for (int i = 0; i < n && i < 32; ++i) {
+        const MfmaTile &t = list[i];
+        if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn) continue;
+        if (t.bm > 2 * pl.p.M + 32 || t.bn > 2 * pl.p.N + 32) continue;
+        emit(t);
+    }
+    return out < cap ? out : cap;
+}
+
+int64_t mb_query(int32_t what) {
+    switch (what) {
+        case MB_QUERY_ABI_VERSION: return MB_ABI_VERSION;
+        case MB_QUERY_HAS_MATRIX_CORES: return dev_info().arch == 950 ? 1 : 0;
+        case MB_QUERY_CU_COUNT: return dev_info().cus;
+        case MB_QUERY_GFX_ARCH: return dev_info().arch;
+        case MB_QUERY_LDS_BYTES: return dev_info().lds;
+    }
+    return MB_ERR_INVALID_ARG;
+}
+
+const char *mb_strerror(int32_t status) {
+    switch (status) {
+        case MB_OK: return "success";
+        case MB_ERR_INVALID_ARG: return "invalid argument";
+        case MB_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype";
+        case MB_ERR_UNSUPPORTED_LAYOUT: return "unsupported layout for the requested backend";
+        case MB_ERR_WORKSPACE: return "workspace missing or too small";
+        case MB_ERR_LAUNCH: return "kernel launch failed";
+        case MB_ERR_NO_DEVICE: return "no HIP device";
+        case MB_ERR_GEMV_SHAPE: return "gemv backend requires M==1 or N==1";
+        case MB_ERR_BAD_BACKEND: return "unknown backend";
+    }
+    return "unknown status";
+}
+
+}  // extern "C"

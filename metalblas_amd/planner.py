@@ -1,0 +1,192 @@
+"""One-shot, correctness-guarded autotuner over the matrix-core tile family.
+
+Restates the reference's autotuner (metalblas/float_dispatch.py:411-481: ``_probe_params``,
+``_fastest``, ``_autotune_mppt``) for gfx950:
+
+  * the C planner's static choice (``mb_plan``) is the primary candidate; the other compiled
+    tiles that fit the shape come from ``mb_tile_candidates`` (re-derived for 256 CUs and
+    160 KB of LDS instead of the Apple tables of float_dispatch.py:369-404);
+  * each candidate runs once and must agree with the primary within 2% of max|C| (exactly,
+    for integer dtypes) before it may be timed (float_dispatch.py:464-468);
+  * a rival replaces the primary only if it is faster by ``margin`` (3%, as
+    float_dispatch.py:157);
+  * the winner is cached per (device, dtype, batch, M, N, K, layout, alignment) key; with
+    ``METALBLAS_PLAN_CACHE=<file>`` the cache persists as JSON across processes.
+
+``METALBLAS_AUTOTUNE=0`` disables tuning (float_dispatch.py:156).  Timing uses HIP events on
+torch's current stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import os
+import threading
+
+import torch
+
+from . import _lib
+
+MARGIN = 0.03
+_MIN_WORK = 1 << 27          # batch*M*N*K below this is not worth timing
+_PLANS: dict = {}
+_LOCK = threading.Lock()
+_CACHE_PATH = os.environ.get("METALBLAS_PLAN_CACHE")
+_loaded = False
+
+
+def enabled() -> bool:
+    return os.environ.get("METALBLAS_AUTOTUNE", "1") != "0"
+
+
+def probe_params(M, N, K):
+    """(warmup, iters, reps) scaled down as kernels get longer (float_dispatch.py:411-418)."""
+    work = M * N * K
+    if work <= 2_000_000_000:
+        return 5, 20, 3
+    if work <= 50_000_000_000:
+        return 2, 5, 3
+    return 1, 3, 2
+
+
+def _load_cache():
+    global _loaded
+    if _loaded:
+        return
+    _loaded = True
+    if not _CACHE_PATH or not os.path.exists(_CACHE_PATH):
+        return
+    try:
+        with open(_CACHE_PATH) as f:
+            data = json.load(f)
+        for k, v in data.items():
+            _PLANS[k] = tuple(v) if v is not None else None
+    except (OSError, ValueError):
+        pass
+
+
+def _save_cache():
+    if not _CACHE_PATH:
+        return
+    tmp = _CACHE_PATH + ".tmp"
+    try:
+        with open(tmp, "w") as f:
+            json.dump({k: (list(v) if v is not None else None) for k, v in _PLANS.items()}, f)
+        os.replace(tmp, _CACHE_PATH)
+    except OSError:
+        pass
+
+
+def _key(desc, device) -> str:
+    def layout(m):
+        return (int(m.col_stride == 1), int(m.row_stride == 1), int((m.ptr or 0) % 16))
+    parts = (device.index if device.index is not None else 0, desc.dtype, desc.batch, desc.M,
+             desc.N, desc.K, layout(desc.a), layout(desc.b), layout(desc.c), desc.epilogue)
+    return "/".join(map(str, parts))
+
+
+def clear():
+    with _LOCK:
+        _PLANS.clear()
+
+
+def cached() -> dict:
+    return dict(_PLANS)
+
+
+def _time(fn, warmup, iters, reps):
+    for _ in range(warmup):
+        fn()
+    best = float("inf")
+    for _ in range(reps):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e) / iters)
+    return best
+
+
+def tune(desc, a, b, out, bias=None) -> None:
+    """Set ``desc.tile`` to the tuned tile for this problem (no-op when not applicable)."""
+    if not enabled():
+        return
+    if desc.batch * desc.M * desc.N * desc.K < _MIN_WORK:
+        return
+    _load_cache()
+    device = out.device
+    key = _key(desc, device)
+    with _LOCK:
+        hit = key in _PLANS
+        tile = _PLANS.get(key)
+    if not hit:
+        with torch.cuda.device(device):
+            tile = _autotune(desc, out)
+        with _LOCK:
+            _PLANS[key] = tile
+            _save_cache()
+    if tile is not None:
+        for i, v in enumerate(tile):
+            desc.tile[i] = int(v)
+
+
+def _autotune(desc, out):
+    info = _lib.plan(desc)
+    if _lib.FAMILY_NAMES.get(info.family) != "mfma":
+        return None
+    cands = _lib.tile_candidates(desc)
+    if len(cands) <= 1:
+        return None
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(out.device).cuda_stream
+    scratch = torch.empty_like(out, memory_format=torch.contiguous_format)
+    ref = torch.empty_like(scratch)
+
+    def runner(tile, dst):
+        d = _lib.MbGemmDesc.from_buffer_copy(desc)
+        for i, v in enumerate(tile):
+            d.tile[i] = int(v)
+        if out.dim() == 3:
+            d.c = _lib.MbMatrix(ctypes.c_void_p(dst.data_ptr()), dst.stride(1), dst.stride(2), dst.stride(0))
+        else:
+            d.c = _lib.MbMatrix(ctypes.c_void_p(dst.data_ptr()), dst.stride(0), dst.stride(1), 0)
+        nbytes = int(lib.mb_gemm_workspace_bytes(ctypes.byref(d)))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=out.device)
+        d.workspace = ctypes.c_void_p(ws.data_ptr())
+        d.workspace_bytes = nbytes
+
+        def fn():
+            _lib.check(lib.mb_gemm(ctypes.byref(d), ctypes.c_void_p(stream)))
+        return fn, ws
+
+    primary_fn, keep0 = runner(cands[0], ref)
+    primary_fn()
+    torch.cuda.synchronize()
+    is_int = out.dtype in (torch.int8, torch.uint8, torch.int16, torch.int32, torch.int64)
+    refv = ref.to(torch.complex64 if ref.is_complex() else torch.float32) if not is_int else ref
+    scale = float(refv.abs().max().item()) + 1e-6 if not is_int else 0.0
+
+    runs = [(cands[0], primary_fn, keep0)]
+    for t in cands[1:]:
+        fn, keep = runner(t, scratch)
+        fn()
+        torch.cuda.synchronize()
+        if is_int:
+            ok = torch.equal(scratch, ref)
+        else:
+            sv = scratch.to(refv.dtype)
+            ok = bool(torch.isfinite(sv).all().item()) and \
+                float((sv - refv).abs().max().item()) <= 0.02 * scale
+        if ok:
+            runs.append((t, fn, keep))
+    if len(runs) == 1:
+        return None
+    bt = out.shape[0] if out.dim() == 3 else 1
+    warmup, iters, reps = probe_params(bt * desc.M, desc.N, desc.K)
+    times = [_time(fn, warmup, iters, reps) for _, fn, _ in runs]
+    best = min(range(len(times)), key=times.__getitem__)
+    if best and times[best] < times[0] * (1.0 - MARGIN):
+        return tuple(runs[best][0])
+    return tuple(runs[0][0])

@@ -1,0 +1,313 @@
+"""GPU parity: metalblas_amd vs the CPU oracle on the same seeded inputs.
+
+Mirrors the coverage matrix of the reference's tests/test_basic.py:166-255 (forced backends,
+transposed layouts, GEMV and strided GEMV, complex64/complex32 with ta/conj, every integer
+dtype, addmm bias shapes and scalar combinations, the beta=0 NaN-leak check, bmm /
+baddbmm / addbmm, N-D broadcasting, dot/vdot/outer/mv).  Inputs are generated on the CPU
+from a seed and copied to the GPU; the oracle sees the same CPU tensors.
+"""
+import pytest
+import torch
+
+import metalblas_amd as mb
+from helpers import ALL, COMPLEX, FLOATS, INTS, assert_parity, gen, rand
+
+pytestmark = pytest.mark.gpu
+
+BASE = [(64, 64, 64), (128, 128, 128), (256, 256, 256), (513, 257, 129), (1024, 1024, 256)]
+
+
+def _matrices(M, N, K, dtype, layout, g):
+    """tests/test_basic.py:72-82."""
+    a = rand((K, M), dtype, g).t() if layout in ("ta", "tr") else rand((M, K), dtype, g)
+    b = rand((N, K), dtype, g).t() if layout == "tr" else rand((K, N), dtype, g)
+    if layout == "conj":
+        a = a.conj()
+    elif layout == "strided":
+        if N == 1:
+            b = rand((K, 2), dtype, g)[:, :1]
+        else:
+            a = rand((K, 2), dtype, g)[:, :1].t()
+    return a, b
+
+
+def _to(t, dev):
+    """Copy to the GPU keeping the view's layout (strides / conj bit)."""
+    if t.is_conj():
+        return _to(t.conj(), dev).conj()
+    base = t.as_strided((t.untyped_storage().nbytes() // t.element_size(),), (1,), 0)
+    return base.to(dev).as_strided(t.shape, t.stride(), t.storage_offset())
+
+
+def check_mm(dev, M, N, K, dtype, backend=None, layout="rm", seed=0):
+    g = gen(seed)
+    a, b = _matrices(M, N, K, dtype, layout, g)
+    kwargs = {"backend": backend} if backend else {}
+    got = mb.matmul(_to(a, dev), _to(b, dev), **kwargs)
+    assert got.dtype == dtype and got.shape == (M, N)
+    assert_parity(got, a, b, tag=f"matmul {dtype} {layout} {backend or 'auto'} {M}x{N}x{K}",
+                  strict=backend not in (None, "mpp"))
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("backend", ["simd", "mpp", "mpp_tensor", "generic", None])
+@pytest.mark.parametrize("shape", BASE + [(33, 33, 33)], ids=str)
+def test_forced_backends(dev, dtype, backend, shape):
+    check_mm(dev, *shape, dtype, backend)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("shape", [(128, 128, 128), (513, 257, 129), (1024, 1024, 256),
+                                   (1, 4096, 4096), (4096, 1, 4096)], ids=str)
+def test_transposed(dev, dtype, shape):
+    check_mm(dev, *shape, dtype, layout="tr")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("shape", [(1, 4096, 4096), (4096, 1, 4096), (1, 1024, 1024), (1024, 1, 1024)],
+                         ids=str)
+def test_gemv_backend(dev, dtype, shape):
+    check_mm(dev, *shape, dtype, backend="gemv")
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("shape", [(1, 1024, 256), (1, 4096, 1024), (64, 1, 256), (1024, 1, 1024)], ids=str)
+def test_gemv_strided(dev, dtype, shape):
+    check_mm(dev, *shape, dtype, backend="gemv", layout="strided")
+
+
+def test_gemv_backend_rejects_matrix(dev):
+    a = torch.randn(8, 8, device=dev)
+    with pytest.raises(ValueError):
+        mb.matmul(a, a, backend="gemv")
+    with pytest.raises(ValueError):
+        mb.matmul(a, a, backend="nope")
+
+
+@pytest.mark.parametrize("shape", [(64, 64, 64), (128, 128, 128), (256, 256, 256), (512, 512, 512),
+                                   (1024, 1024, 1024), (513, 257, 129), (333, 444, 555), (2, 64, 128),
+                                   (1, 4096, 4096), (4096, 1, 4096), (1, 1024, 1024), (1024, 1, 1024),
+                                   (1, 1, 512), (1, 17, 33)], ids=str)
+def test_complex64(dev, shape):
+    check_mm(dev, *shape, torch.complex64)
+
+
+@pytest.mark.parametrize("layout", ["ta", "conj"])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (513, 257, 129)], ids=str)
+def test_complex64_layouts(dev, shape, layout):
+    check_mm(dev, *shape, torch.complex64, layout=layout)
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 256), (512, 512, 512), (1, 2048, 2048), (2048, 1, 2048)], ids=str)
+def test_complex32(dev, shape):
+    check_mm(dev, *shape, torch.complex32)
+
+
+@pytest.mark.parametrize("dtype", INTS, ids=str)
+@pytest.mark.parametrize("shape", [(64, 64, 64), (256, 256, 256), (513, 257, 129), (333, 444, 555),
+                                   (1024, 1024, 1024), (96, 4096, 512), (33, 33, 33), (1, 4096, 4096),
+                                   (4096, 1, 4096), (1, 1024, 257), (300, 1, 1024)], ids=str)
+def test_integers(dev, dtype, shape):
+    check_mm(dev, *shape, dtype)
+
+
+@pytest.mark.parametrize("dtype", INTS, ids=str)
+def test_integers_transposed(dev, dtype):
+    check_mm(dev, 256, 256, 256, dtype, layout="ta")
+
+
+# ---- fused ops (tests/test_basic.py:106-137, 202-242) ----------------------------------------
+
+def check_fused(dev, op, shape, dtype, bshape, beta=1, alpha=1, seed=0):
+    g = gen(seed)
+    if op == "addmm":
+        M, N, K = shape
+        a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    else:
+        Bb, M, N, K = shape
+        a, b = rand((Bb, M, K), dtype, g), rand((Bb, K, N), dtype, g)
+    bias = rand(bshape, dtype, g)
+    got = getattr(mb, op)(bias.to(dev), a.to(dev), b.to(dev), beta=beta, alpha=alpha)
+    tag = f"{op} {dtype} {shape} bias={bshape} beta={beta} alpha={alpha}"
+    # scalars as metalblas/dispatch.py:146-150 casts them
+    if dtype in INTS:
+        cb, ca = int(beta), int(alpha)
+    elif dtype in COMPLEX:
+        cb, ca = beta, alpha
+    else:
+        cb, ca = float(beta), float(alpha)
+    if op == "addbmm":
+        Bb, M, N, K = shape
+        a2 = a.permute(1, 0, 2).reshape(M, Bb * K)
+        b2 = b.reshape(Bb * K, N)
+        assert_parity(got, a2, b2, bias=bias, beta=cb, alpha=ca, tag=tag)
+    else:
+        assert_parity(got, a, b, bias=bias, beta=cb, alpha=ca, tag=tag)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+@pytest.mark.parametrize("bshape", [(128, 96), (1, 96), (128, 1), (96,), (1,), ()], ids=str)
+def test_addmm_bias_shapes(dev, dtype, bshape):
+    check_fused(dev, "addmm", (128, 96, 256), dtype, bshape)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+@pytest.mark.parametrize("ba", [(2, 3), (0, 1), (1, 0), (0, 0)], ids=str)
+def test_addmm_scalars(dev, dtype, ba):
+    check_fused(dev, "addmm", (128, 96, 256), dtype, (96,), *ba)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+def test_addmm_gemv(dev, dtype):
+    check_fused(dev, "addmm", (1, 4096, 4096), dtype, (4096,))
+    check_fused(dev, "addmm", (4096, 1, 4096), dtype, (1,))
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("mnk", [(130, 100, 200), (257, 257, 257), (333, 444, 555)], ids=str)
+def test_addmm_odd(dev, dtype, mnk):
+    M, N, K = mnk
+    for bshape in [(M, N), (1, N), (M, 1), (N,), (1,), ()]:
+        check_fused(dev, "addmm", (M, N, K), dtype, bshape)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+def test_addmm_beta0_nan_bias(dev, dtype):
+    """tests/test_basic.py:214-217: beta == 0 must not read the bias."""
+    g = gen(0)
+    a, b = rand((128, 256), dtype, g).to(dev), rand((256, 96), dtype, g).to(dev)
+    got = mb.addmm(torch.full((128, 96), float("nan"), dtype=dtype, device=dev), a, b, beta=0)
+    assert not torch.isnan(got).any().item()
+
+
+BMM_SHAPES = [(8, 128, 128, 128), (32, 256, 256, 256), (4, 512, 512, 512), (96, 512, 512, 64),
+              (16, 64, 4096, 512), (128, 4096, 64, 256), (512, 64, 64, 64), (2048, 64, 64, 32),
+              (3, 130, 100, 200), (8, 1, 512, 256), (8, 512, 1, 256)]
+
+
+def check_bmm(dev, Bb, M, N, K, dtype, layout="rm", seed=0):
+    g = gen(seed)
+    if layout == "tr":
+        a = rand((Bb, K, M), dtype, g).transpose(-2, -1)
+        b = rand((Bb, N, K), dtype, g).transpose(-2, -1)
+    else:
+        a, b = rand((Bb, M, K), dtype, g), rand((Bb, K, N), dtype, g)
+    got = mb.bmm(_to(a, dev), _to(b, dev))
+    assert_parity(got, a, b, tag=f"bmm {dtype} {layout} {Bb}x{M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+@pytest.mark.parametrize("shape", BMM_SHAPES, ids=str)
+def test_bmm(dev, dtype, shape):
+    check_bmm(dev, *shape, dtype)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+def test_bmm_transposed(dev, dtype):
+    check_bmm(dev, 8, 256, 256, 256, dtype, "tr")
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+@pytest.mark.parametrize("bshape", [(4, 128, 96), (4, 1, 96), (4, 128, 1), (1, 128, 96), (128, 96), (96,),
+                                    (1,), ()], ids=str)
+def test_baddbmm_bias_shapes(dev, dtype, bshape):
+    check_fused(dev, "baddbmm", (4, 128, 96, 256), dtype, bshape)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+@pytest.mark.parametrize("ba", [(2, 3), (0, 1), (1, 0), (0, 0)], ids=str)
+def test_baddbmm_scalars(dev, dtype, ba):
+    check_fused(dev, "baddbmm", (4, 128, 96, 256), dtype, (96,), *ba)
+
+
+@pytest.mark.parametrize("dtype", ALL, ids=str)
+def test_addbmm(dev, dtype):
+    for bshape in [(128, 96), (1, 96), (128, 1), (96,), (1,), ()]:
+        check_fused(dev, "addbmm", (8, 128, 96, 256), dtype, bshape)
+    for shape in [(32, 64, 64, 64), (4, 256, 256, 512)]:
+        check_fused(dev, "addbmm", shape, dtype, (shape[2],))
+    for ba in [(1, 1), (2, 3), (0, 1), (1, 0)]:
+        check_fused(dev, "addbmm", (8, 128, 96, 256), dtype, (96,), *ba)
+
+
+@pytest.mark.parametrize("dtype", FLOATS, ids=str)
+@pytest.mark.parametrize("mnk", [(130, 100, 200), (257, 129, 257)], ids=str)
+def test_baddbmm_odd(dev, dtype, mnk):
+    M, N, K = mnk
+    for bshape in [(4, M, N), (N,), ()]:
+        check_fused(dev, "baddbmm", (4, M, N, K), dtype, bshape)
+
+
+# ---- N-D broadcasting and vector helpers (tests/test_basic.py:140-163, 244-255) ------------
+
+ND_CASES = [((64,), (64,)), ((32,), (32, 48)), ((40, 32), (32,)), ((32,), (8, 32, 48)),
+            ((6, 40, 32), (32,)), ((8, 40, 32), (8, 32, 48)), ((8, 40, 32), (32, 48)),
+            ((40, 32), (8, 32, 48)), ((2, 3, 40, 32), (2, 3, 32, 48)), ((3, 1, 64, 32), (1, 5, 32, 48))]
+
+
+def _torch_ref_nd(a, b):
+    """Broadcast with torch on CPU, then run the oracle on the 3-D/2-D form."""
+    a2 = a.unsqueeze(0) if a.dim() == 1 else a
+    b2 = b.unsqueeze(-1) if b.dim() == 1 else b
+    batch = torch.broadcast_shapes(a2.shape[:-2], b2.shape[:-2])
+    M, K = a2.shape[-2:]
+    N = b2.shape[-1]
+    return a2, b2, batch, M, N, K
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.complex64,
+                                   torch.int32, torch.int8, torch.int64], ids=str)
+@pytest.mark.parametrize("shapes", ND_CASES, ids=str)
+def test_nd_broadcast(dev, dtype, shapes):
+    g = gen(0)
+    a, b = rand(shapes[0], dtype, g), rand(shapes[1], dtype, g)
+    got = mb.matmul(a.to(dev), b.to(dev))
+    expect_shape = torch.matmul(a.to(torch.float32 if dtype not in COMPLEX else torch.complex64),
+                                b.to(torch.float32 if dtype not in COMPLEX else torch.complex64)).shape
+    assert got.shape == expect_shape and got.dtype == dtype
+    a2, b2, batch, M, N, K = _torch_ref_nd(a, b)
+    if batch:
+        size = 1
+        for s in batch:
+            size *= s
+        a3 = a2.expand(*batch, M, K).reshape(size, M, K)
+        b3 = b2.expand(*batch, K, N).reshape(size, K, N)
+        assert_parity(got.reshape(size, M, N), a3, b3, tag=f"nd {dtype} {shapes}")
+    else:
+        assert_parity(got.reshape(M, N), a2, b2, tag=f"nd {dtype} {shapes}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.complex64,
+                                   torch.complex32, torch.int8, torch.int32, torch.int64], ids=str)
+def test_vectors(dev, dtype):
+    g = gen(0)
+    for k in (4096, 7, 1):
+        a, b = rand((k,), dtype, g), rand((k,), dtype, g)
+        got = mb.dot(a.to(dev), b.to(dev))
+        assert got.shape == () and got.dtype == dtype
+        assert_parity(got.reshape(1, 1), a.reshape(1, k), b.reshape(k, 1), tag=f"dot {dtype} {k}")
+        got = mb.vdot(a.to(dev), b.to(dev))
+        assert got.shape == ()
+        assert_parity(got.reshape(1, 1), a.reshape(1, k).conj() if dtype in COMPLEX else a.reshape(1, k),
+                      b.reshape(k, 1), tag=f"vdot {dtype} {k}")
+    a, b = rand((128,), dtype, g), rand((96,), dtype, g)
+    got = mb.outer(a.to(dev), b.to(dev))
+    assert got.shape == (128, 96)
+    assert_parity(got, a.reshape(128, 1), b.reshape(1, 96), k=1, tag=f"outer {dtype}")
+    a, b = rand((256, 512), dtype, g), rand((512,), dtype, g)
+    got = mb.mv(a.to(dev), b.to(dev))
+    assert got.shape == (256,)
+    assert_parity(got.reshape(256, 1), a, b.reshape(512, 1), tag=f"mv {dtype}")
+
+
+def test_empty_and_k0(dev):
+    """metalblas/dispatch.py:234-237: empty batch -> empty, K == 0 -> zeros."""
+    a = torch.randn(3, 4, 0, device=dev)
+    b = torch.randn(3, 0, 5, device=dev)
+    r = mb.bmm(a, b)
+    assert r.shape == (3, 4, 5) and bool((r == 0).all())
+    r = mb.bmm(torch.randn(0, 4, 2, device=dev), torch.randn(0, 2, 5, device=dev))
+    assert r.shape == (0, 4, 5)
+    bias = torch.randn(5, device=dev)
+    r = mb.addmm(bias, torch.randn(4, 0, device=dev), torch.randn(0, 5, device=dev), beta=2.0)
+    assert torch.allclose(r, (2.0 * bias).expand(4, 5))
