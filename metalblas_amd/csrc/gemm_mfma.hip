@@ -12,16 +12,47 @@ hipError_t launch_f32(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipS
 hipError_t launch_i8(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_u8(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 }  // namespace mfma
+namespace m16 {
+hipError_t launch_bf16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_bf16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_f16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_f16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+}  // namespace m16
 
 namespace {
 // ---- compiled tile table ----------------------------------------------------------------
 struct TileEntry {
     int bm, bn, wm, wn;
 };
+// register-staged family (mfma_gemm.hpp): every matrix-core dtype
 constexpr TileEntry kTiles[] = {
     {256, 256, 2, 2}, {256, 128, 2, 2}, {128, 256, 2, 2}, {128, 128, 2, 2},
     {128, 64, 2, 2},  {64, 128, 2, 2},  {64, 64, 2, 2},   {32, 32, 1, 1},
 };
+// LDS-direct 16-bit family (mfma16.hpp): bf16 / fp16
+constexpr TileEntry kTiles16[] = {
+    {256, 256, 2, 2}, {256, 256, 2, 4}, {256, 128, 2, 2}, {128, 256, 2, 2},
+    {128, 128, 2, 2}, {128, 64, 2, 2},  {64, 128, 2, 2},  {64, 64, 2, 2},  {32, 32, 1, 1},
+};
+
+bool is16(int dt) { return dt == BF16 || dt == F16; }
+
+bool in_table(const TileEntry *tb, int n, const MfmaTile &t) {
+    for (int i = 0; i < n; ++i)
+        if (tb[i].bm == t.bm && tb[i].bn == t.bn && tb[i].wm == t.wm && tb[i].wn == t.wn) return true;
+    return false;
+}
+
+// The LDS-direct loads address each operand tile with 31-bit byte offsets from the tile's
+// first element; larger spans take the register-staged kernel.
+bool m16_offsets_fit(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g) {
+    const int64_t lim = (int64_t)1 << 30;
+    const int64_t lda = a_kc ? g.a_rs : g.a_cs, ldb = b_kc ? g.b_cs : g.b_rs;
+    const int64_t K = (int64_t)g.k_chunk + 64;
+    const int64_t ea = a_kc ? (int64_t)t.bm * lda + K : K * lda + t.bm;
+    const int64_t eb = b_kc ? (int64_t)t.bn * ldb + K : K * ldb + t.bn;
+    return ea * 2 < lim && eb * 2 < lim;
+}
 
 }  // namespace
 
@@ -29,16 +60,17 @@ bool mfma_supported_dtype(int dt) { return dt == BF16 || dt == F16 || dt == F32 
 
 int mfma_k_align(int dt) { return 16 / dtype_size(dt); }
 
-bool mfma_tile_compiled(int, const MfmaTile &t) {
-    for (const auto &e : kTiles)
-        if (e.bm == t.bm && e.bn == t.bn && e.wm == t.wm && e.wn == t.wn) return true;
-    return false;
+bool mfma_tile_compiled(int dt, const MfmaTile &t) {
+    if (is16(dt)) return in_table(kTiles16, sizeof(kTiles16) / sizeof(kTiles16[0]), t);
+    return in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t);
 }
 
-int mfma_list_tiles(int, MfmaTile *out, int cap) {
+int mfma_list_tiles(int dt, MfmaTile *out, int cap) {
+    const TileEntry *tb = is16(dt) ? kTiles16 : kTiles;
+    const int cnt = is16(dt) ? (int)(sizeof(kTiles16) / sizeof(kTiles16[0])) : (int)(sizeof(kTiles) / sizeof(kTiles[0]));
     int n = 0;
-    for (const auto &e : kTiles) {
-        if (n < cap) out[n] = {e.bm, e.bn, e.wm, e.wn};
+    for (int i = 0; i < cnt; ++i) {
+        if (n < cap) out[n] = {tb[i].bm, tb[i].bn, tb[i].wm, tb[i].wn};
         ++n;
     }
     return n;
@@ -49,6 +81,21 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
     const int tiles = cdiv(g.M, t.bm) * cdiv(g.N, t.bn);
     dim3 grid(tiles, g.splits, g.batch < 65535 ? g.batch : 65535);
     if (shape) *shape = {grid, dim3(64 * t.wm * t.wn)};
+    if (is16(dt) && !(t.bm == 32 && t.bn == 32)) {
+        if (m16_offsets_fit(t, a_kc, b_kc, g)) {
+            const bool whole = (g.k_chunk % 64) == 0 && (g.K % 64) == 0;
+            if (dt == BF16)
+                return whole ? m16::launch_bf16_kwhole(t, a_kc, b_kc, g, grid, st)
+                             : m16::launch_bf16_ktail(t, a_kc, b_kc, g, grid, st);
+            return whole ? m16::launch_f16_kwhole(t, a_kc, b_kc, g, grid, st)
+                         : m16::launch_f16_ktail(t, a_kc, b_kc, g, grid, st);
+        }
+        // very large leading dimensions: register-staged kernel with a compiled 4-wave tile
+        MfmaTile v = in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t) ? t : MfmaTile{128, 128, 2, 2};
+        dim3 grid2(cdiv(g.M, v.bm) * cdiv(g.N, v.bn), g.splits, grid.z);
+        if (shape) *shape = {grid2, dim3(64 * v.wm * v.wn)};
+        return dt == BF16 ? mfma::launch_bf16(v, a_kc, b_kc, g, grid2, st) : mfma::launch_f16(v, a_kc, b_kc, g, grid2, st);
+    }
     switch (dt) {
         case BF16: return mfma::launch_bf16(t, a_kc, b_kc, g, grid, st);
         case F16: return mfma::launch_f16(t, a_kc, b_kc, g, grid, st);

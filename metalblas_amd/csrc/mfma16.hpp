@@ -1,0 +1,419 @@
+// Matrix-core GEMM for 16-bit inputs (bf16 / fp16) on gfx950, fed by LDS-direct loads.
+//
+// Differences from the register-staged matrix-core template (mfma_gemm.hpp):
+//   * Operand tiles go from global memory straight into LDS with buffer_load_dwordx4 ... lds
+//     (64 lanes x 16 bytes = 1 KiB per instruction, lane-contiguous in LDS).  No staging
+//     registers and no register transposes: the LDS layout is chosen by giving each lane the
+//     global chunk that belongs at its LDS slot.  Rows past the matrix edge use a buffer
+//     offset beyond the resource's range, which the hardware turns into zeros.  The per-lane
+//     offsets are loop invariant; the K advance of each stage travels in the uniform
+//     soffset operand.
+//   * Operands contiguous along K are stored K-major (one 128-byte row per M/N index,
+//     16-byte chunks XOR-swizzled by (row & 7) ^ ((row >> 3) & 3), periodic in 32 rows) and
+//     read as 16-byte fragments (ds_read_b128).
+//   * Operands contiguous along M/N are stored M/N-major (one row per k) and read with
+//     ds_read_b64_tr_b16: each 16-lane group transposes a 4 (k) x 16 (m/n) block, so two
+//     such reads give a lane the 8 consecutive k of one column that the 32x32x16 MFMA
+//     expects.  Chunks are XOR-swizzled by k % 4 with {0, 4, 10, 14}, which keeps a 16-lane
+//     and a 32-lane slice of one read on distinct 16-byte bank groups.
+//   * Stage pipeline: two LDS buffers; the loads of stage kt+2 are issued right after the
+//     barrier that retires stage kt, and the MFMAs of the last k-step of stage kt are issued
+//     after that barrier so they cover the latency of the first fragment reads of kt+1.
+//   * C^T = B^T A^T product for 4-wide output stores, fused epilogue, split-K partial planes,
+//     batching and the XCD-aware tile order are shared with mfma_gemm.hpp.
+#pragma once
+
+#include "launch.hpp"
+
+namespace mb {
+namespace m16 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+#define MB_LDS __attribute__((address_space(3)))
+
+__device__ void raw_buffer_load_lds(i32x4 rsrc, MB_LDS uint32_t *lds, int size, int voffset, int soffset,
+                                    int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
+constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that is always out of range
+
+struct __attribute__((packed)) BufRes {
+    const void *base;
+    uint32_t range;
+    uint32_t config;
+};
+__device__ __forceinline__ i32x4 make_rsrc(const void *base) {
+    BufRes r{base, 0x7fffffffu, 0x00020000u};
+    return __builtin_bit_cast(i32x4, r);
+}
+
+template <class T> __device__ __forceinline__ void mma16(f32x16 &c, uint4 a, uint4 b);
+template <> __device__ __forceinline__ void mma16<bf16_t>(f32x16 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                0, 0, 0);
+}
+template <> __device__ __forceinline__ void mma16<f16_t>(f32x16 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                               0, 0);
+}
+
+__device__ __forceinline__ int swz_k(int row) { return (row & 7) ^ ((row >> 3) & 3); }
+template <int CPR> __device__ __forceinline__ int swz_mn(int k) {
+    // {0, 4, 10, 14}[k & 3], limited to the chunks of one row
+    const int f = ((k & 1) << 2) | ((k & 2) ? 10 : 0);
+    return f & (CPR - 1);
+}
+
+__device__ __forceinline__ MB_LDS char *lds_ptr(const char *p) { return (MB_LDS char *)(MB_LDS void *)p; }
+
+// One operand tile: ROWS (M or N) x 64 k, 16-bit elements.
+template <int ROWS, int NW, bool KC> struct Tile16 {
+    static constexpr int BYTES = ROWS * 128;
+    static constexpr int SEGS = BYTES / 1024;      // 1 KiB direct-load segments
+    static constexpr int PER_WAVE = (SEGS + NW - 1) / NW;
+    static constexpr int RB = ROWS * 2;            // MN-major row bytes
+    static constexpr int CPR = RB / 16;            // MN-major chunks per row
+    static_assert(ROWS % 32 == 0 && (KC || ROWS >= 64), "tile rows");
+
+    // Byte offset (relative to the resource base = element (row0, k0)) of the chunk a lane
+    // loads for segment `seg`, or kOOB.
+    __device__ __forceinline__ static uint32_t src_offset(int seg, int lane, int64_t ld, int rows_left,
+                                                          int k_left) {
+        const int byte = seg * 1024 + lane * 16;
+        if constexpr (KC) {
+            const int r = byte >> 7, p = (byte >> 4) & 7;
+            const int c = p ^ swz_k(r);
+            if (r >= rows_left || c * 8 >= k_left) return kOOB;
+            return (uint32_t)(((int64_t)r * ld + c * 8) * 2);
+        } else {
+            const int k = byte / RB, p = (byte % RB) >> 4;
+            const int c = p ^ swz_mn<CPR>(k);
+            if (k >= k_left || c * 8 >= rows_left) return kOOB;
+            return (uint32_t)(((int64_t)k * ld + c * 8) * 2);
+        }
+    }
+
+    // Lane-dependent LDS byte offset of the fragment of MFMA block `j` (32 rows) at k-step 0;
+    // k-steps and blocks j' = j (mod 2 for KC) add compile-time constants.
+    __device__ __forceinline__ static int frag_base(int row0, int lane, int j) {
+        if constexpr (KC) {
+            const int row = row0 + (lane & 31);
+            return row * 128;   // chunk part is added per step (swizzle depends on lane only)
+        } else {
+            const int kr = (lane & 15) >> 2;   // k row within the 4-row group
+            const int col = row0 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+            return (kr + 8 * (lane >> 5)) * RB + (((col >> 3) ^ swz_mn<CPR>(kr)) << 4) + ((col & 7) << 1);
+        }
+    }
+
+    __device__ __forceinline__ static uint4 frag(const char *lds, int base, int lane, int s, int j) {
+        if constexpr (KC) {
+            const int row = lane & 31;   // swizzle is periodic in 32 rows
+            const int chunk = (2 * s + (lane >> 5)) ^ swz_k(row);
+            return *(const uint4 *)(lds + base + j * 32 * 128 + (chunk << 4));
+        } else {
+            uint4 out;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                // k = 16 s + 8 (lane / 32) + 4 t + kr; the lane terms are folded into base
+                const int koff = (16 * s + 4 * t) * RB;
+                bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
+                uint2 u = __builtin_bit_cast(uint2, v);
+                if (t == 0) {
+                    out.x = u.x;
+                    out.y = u.y;
+                } else {
+                    out.z = u.x;
+                    out.w = u.y;
+                }
+            }
+            return out;
+        }
+    }
+};
+
+__device__ __forceinline__ void tile_coords16(int pid, int tiles_m, int tiles_n, int swz, int &tm, int &tn) {
+    const int n = tiles_m * tiles_n;
+    if (n >= 16) {
+        const int xcd = pid & 7, idx = pid >> 3;
+        const int base = n >> 3, rem = n & 7;
+        pid = xcd * base + min(xcd, rem) + idx;
+    }
+    const int G = 1 << swz;
+    const int width = G * tiles_n;
+    const int grp = pid / width;
+    const int first_m = grp * G;
+    const int gsz = min(tiles_m - first_m, G);
+    const int in = pid - grp * width;
+    tm = first_m + in % gsz;
+    tn = in / gsz;
+}
+
+// KTAIL: some K slice ends inside a 64-wide stage (its last stage is zero-filled past the
+// edge).  Without it the main loop carries no edge logic.
+template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
+    constexpr int NW = WM * WN;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int BK = 64;
+    using TA = Tile16<BM, NW, A_KC>;
+    using TB = Tile16<BN, NW, B_KC>;
+    constexpr int STAGE = TA::BYTES + TB::BYTES;
+    static_assert(TM >= 1 && TN >= 1, "wave tile");
+    // LDS read instructions per k-step (a transposing fragment takes two)
+    constexpr int NREAD_RAW = TM * (A_KC ? 1 : 2) + TN * (B_KC ? 1 : 2);
+    constexpr int NREAD = NREAD_RAW < TM * TN ? NREAD_RAW : TM * TN;
+
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const int tiles_m = cdiv(g.M, BM), tiles_n = cdiv(g.N, BN);
+    int tm, tn;
+    tile_coords16(blockIdx.x, tiles_m, tiles_n, g.swz, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.k_chunk;
+    const int kend = min(g.K, kbeg + g.k_chunk);
+    const int klen = kend - kbeg;
+    const int nk = cdiv(klen, BK);
+    const int nfull = klen / BK;   // stages without a K edge
+    const int64_t lda = A_KC ? g.a_rs : g.a_cs;
+    const int64_t ldb = B_KC ? g.b_cs : g.b_rs;
+    const int rows_a = g.M - m0, rows_b = g.N - n0;
+    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * 2);
+    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * 2);
+
+    // loop-invariant per-lane source offsets (full stages)
+    uint32_t offa[TA::PER_WAVE], offb[TB::PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < TA::PER_WAVE; ++i) {
+        const int seg = wave + i * NW;
+        offa[i] = seg < TA::SEGS ? TA::src_offset(seg, lane, lda, rows_a, BK) : kOOB;
+    }
+#pragma unroll
+    for (int i = 0; i < TB::PER_WAVE; ++i) {
+        const int seg = wave + i * NW;
+        offb[i] = seg < TB::SEGS ? TB::src_offset(seg, lane, ldb, rows_b, BK) : kOOB;
+    }
+    // lane-dependent LDS fragment offsets
+    int fba[A_KC ? 1 : TM], fbb[B_KC ? 1 : TN];
+#pragma unroll
+    for (int j = 0; j < (A_KC ? 1 : TM); ++j) fba[j] = TA::frag_base(wm * WTM, lane, j);
+#pragma unroll
+    for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
+
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
+        // resource bases: element (row0, kbeg) of each operand tile
+        const T *Ab = (const T *)g.a + bz * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
+        const T *Bb = (const T *)g.b + bz * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
+        const i32x4 ra = make_rsrc(Ab), rb = make_rsrc(Bb);
+
+        auto load_stage = [&](int kt, int buf) {
+            char *base = smem + buf * STAGE;
+            if (!KTAIL || kt < nfull) {
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i) {
+                    const int seg = wave + i * NW;
+                    if (TA::SEGS % NW == 0 || seg < TA::SEGS)
+                        raw_buffer_load_lds(ra, (MB_LDS uint32_t *)lds_ptr(base + seg * 1024), 16, (int)offa[i],
+                                            kt * stepa, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i) {
+                    const int seg = wave + i * NW;
+                    if (TB::SEGS % NW == 0 || seg < TB::SEGS)
+                        raw_buffer_load_lds(rb, (MB_LDS uint32_t *)lds_ptr(base + TA::BYTES + seg * 1024), 16,
+                                            (int)offb[i], kt * stepb, 0, 0);
+                }
+            } else {
+                // the K edge: chunks past the slice end read as zeros
+                const int kleft = klen - kt * BK;
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i) {
+                    const int seg = wave + i * NW;
+                    if (TA::SEGS % NW == 0 || seg < TA::SEGS)
+                        raw_buffer_load_lds(ra, (MB_LDS uint32_t *)lds_ptr(base + seg * 1024), 16,
+                                            (int)TA::src_offset(seg, lane, lda, rows_a, kleft), kt * stepa, 0, 0);
+                }
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i) {
+                    const int seg = wave + i * NW;
+                    if (TB::SEGS % NW == 0 || seg < TB::SEGS)
+                        raw_buffer_load_lds(rb, (MB_LDS uint32_t *)lds_ptr(base + TA::BYTES + seg * 1024), 16,
+                                            (int)TB::src_offset(seg, lane, ldb, rows_b, kleft), kt * stepb, 0, 0);
+                }
+            }
+        };
+
+        f32x16 acc[TN][TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        uint4 fa[2][TM], fb[2][TN];
+        auto read_frags = [&](const char *cur, int s, int slot) {
+#pragma unroll
+            for (int j = 0; j < TM; ++j) fa[slot][j] = TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
+#pragma unroll
+            for (int i = 0; i < TN; ++i) fb[slot][i] = TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
+        };
+        auto mma_step = [&](int slot) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[slot][i], fa[slot][j]);
+        };
+
+        if (nk > 0) {
+            load_stage(0, 0);
+            __syncthreads();
+            read_frags(smem, 0, 0);
+            if (nk > 1) load_stage(1, 1);
+        }
+        for (int kt = 0; kt < nk; ++kt) {
+            const char *cur = smem + (kt & 1) * STAGE;
+#pragma unroll
+            for (int s = 0; s < 3; ++s) {
+                read_frags(cur, s + 1, (s + 1) & 1);
+                mma_step(s & 1);
+                // one fragment read after each MFMA, so the reads of step s+1 spread over the
+                // MFMAs of step s instead of stalling in a clump
+#pragma unroll
+                for (int r = 0; r < NREAD; ++r) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - NREAD, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (kt + 1 < nk) {
+                __syncthreads();   // stage kt+1 landed everywhere; stage kt fully read
+                __builtin_amdgcn_sched_barrier(0);
+                read_frags(smem + ((kt + 1) & 1) * STAGE, 0, 0);
+                if (kt + 2 < nk) load_stage(kt + 2, kt & 1);
+            }
+            mma_step(1);
+        }
+
+        // ---- epilogue: lane holds C[m][n_blk + 8*(r/4) + 4*(lane/32) + r%4] ----
+        const int mrow = lane & 31;
+        const int nsub = 4 * (lane >> 5);
+        T *Cb = (T *)g.c + bz * g.c_bs;
+        if (g.splits > 1) {
+            float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
+            const bool vec = (g.N & 3) == 0;
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int gm = m0 + wm * WTM + j * 32 + mrow;
+                    if (gm >= g.M) continue;
+                    float *row = ws + (int64_t)gm * g.N;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
+                        if (vec && gn + 3 < g.N) {
+                            *(float4 *)(row + gn) = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                                acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (gn + r < g.N) row[gn + r] = acc[i][j][4 * q + r];
+                        }
+                    }
+                }
+        } else if (g.vec_ok && !g.epilogue) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int gm = m0 + wm * WTM + j * 32 + mrow;
+                    if (gm >= g.M) continue;
+                    T *row = Cb + gm * g.c_rs;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
+                        if (gn + 3 < g.N) {
+                            T o[4];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
+                            uint2 u;
+                            __builtin_memcpy(&u, o, 8);
+                            *(uint2 *)(row + gn) = u;
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (gn + r < g.N) row[gn + r] = (T)acc[i][j][4 * q + r];
+                        }
+                    }
+                }
+        } else {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) {
+                    const int gm = m0 + wm * WTM + j * 32 + mrow;
+                    if (gm >= g.M) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int n = gn + r;
+                            if (n < g.N)
+                                store_out<T>(g, Cb + gm * g.c_rs + n * g.c_cs, acc[i][j][4 * q + r],
+                                             bz * g.bias_bs + gm * g.bias_rs + n * g.bias_cs);
+                        }
+                    }
+                }
+        }
+        __syncthreads();   // LDS reuse by the next batch iteration
+    }
+}
+
+template <class T, int BM, int BN, int WM, int WN, bool KTAIL>
+hipError_t launch16(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    dim3 block(64 * WM * WN);
+    if (a_kc && b_kc)
+        hipLaunchKernelGGL((k_gemm16<T, BM, BN, WM, WN, true, true, KTAIL>), grid, block, 0, st, g);
+    else if (a_kc && !b_kc)
+        hipLaunchKernelGGL((k_gemm16<T, BM, BN, WM, WN, true, false, KTAIL>), grid, block, 0, st, g);
+    else if (!a_kc && b_kc)
+        hipLaunchKernelGGL((k_gemm16<T, BM, BN, WM, WN, false, true, KTAIL>), grid, block, 0, st, g);
+    else
+        hipLaunchKernelGGL((k_gemm16<T, BM, BN, WM, WN, false, false, KTAIL>), grid, block, 0, st, g);
+    return hipGetLastError();
+}
+
+// Compiled 16-bit tiles: (BM, BN, WM, WN)
+#define MB_M16_TILES(X) \
+    X(256, 256, 2, 2)   \
+    X(256, 256, 2, 4)   \
+    X(256, 128, 2, 2)   \
+    X(128, 256, 2, 2)   \
+    X(128, 128, 2, 2)   \
+    X(128, 64, 2, 2)    \
+    X(64, 128, 2, 2)    \
+    X(64, 64, 2, 2)
+
+template <class T, bool KTAIL>
+hipError_t launch16_typed(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+#define MB_M16_CASE(BM, BN, WM, WN) \
+    if (t.bm == BM && t.bn == BN && t.wm == WM && t.wn == WN) \
+        return launch16<T, BM, BN, WM, WN, KTAIL>(a_kc, b_kc, g, grid, st);
+    MB_M16_TILES(MB_M16_CASE)
+#undef MB_M16_CASE
+    return hipErrorInvalidValue;
+}
+
+}  // namespace m16
+}  // namespace mb
