@@ -110,20 +110,44 @@ __global__ __launch_bounds__(256) void k_fill(GemmArgs g) {
     }
 }
 
-// Split-K: C = epilogue(sum_s ws[s]) with a fixed summation order (deterministic).
-template <class T>
+// Split-K: C = epilogue(sum_s ws[s]).  TPO threads share one output: thread `sub` sums
+// planes sub, sub+TPO, ... (four independent partial sums), and the TPO partials are added
+// in a fixed order through LDS, so the result is deterministic.  Threads with the same sub
+// read consecutive outputs (coalesced).
+template <class T, int TPO>
 __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
     using A = typename Tr<T>::acc;
+    constexpr int OPB = 256 / TPO;   // outputs per block iteration
+    __shared__ A part[TPO][OPB];
     const int64_t plane = (int64_t)g.batch * g.M * g.N;
     const A *ws = (const A *)g.ws;
-    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < plane; i += (int64_t)gridDim.x * 256) {
-        A v = ws[i];
-        for (int s = 1; s < g.splits; ++s) v = acc_add(v, ws[s * plane + i]);
-        const int64_t bz = i / ((int64_t)g.M * g.N);
-        const int64_t r = i % ((int64_t)g.M * g.N);
-        const int64_t m = r / g.N, n = r % g.N;
-        T *c = (T *)g.c + bz * g.c_bs + m * g.c_rs + n * g.c_cs;
-        store_out<T>(g, c, v, bz * g.bias_bs + m * g.bias_rs + n * g.bias_cs);
+    const int sub = threadIdx.x / OPB, oi = threadIdx.x % OPB;
+    for (int64_t base = (int64_t)blockIdx.x * OPB; base < plane; base += (int64_t)gridDim.x * OPB) {
+        const int64_t i = base + oi;
+        A v0 = Tr<T>::zero(), v1 = v0, v2 = v0, v3 = v0;
+        if (i < plane) {
+            int s = sub;
+            for (; s + 3 * TPO < g.splits; s += 4 * TPO) {
+                v0 = acc_add(v0, ws[(int64_t)s * plane + i]);
+                v1 = acc_add(v1, ws[(int64_t)(s + TPO) * plane + i]);
+                v2 = acc_add(v2, ws[(int64_t)(s + 2 * TPO) * plane + i]);
+                v3 = acc_add(v3, ws[(int64_t)(s + 3 * TPO) * plane + i]);
+            }
+            for (; s < g.splits; s += TPO) v0 = acc_add(v0, ws[(int64_t)s * plane + i]);
+        }
+        part[sub][oi] = acc_add(acc_add(v0, v1), acc_add(v2, v3));
+        __syncthreads();
+        if (sub == 0 && i < plane) {
+            A v = part[0][oi];
+#pragma unroll
+            for (int q = 1; q < TPO; ++q) v = acc_add(v, part[q][oi]);
+            const int64_t bz = i / ((int64_t)g.M * g.N);
+            const int64_t r = i % ((int64_t)g.M * g.N);
+            const int64_t m = r / g.N, n = r % g.N;
+            T *c = (T *)g.c + bz * g.c_bs + m * g.c_rs + n * g.c_cs;
+            store_out<T>(g, c, v, bz * g.bias_bs + m * g.bias_rs + n * g.bias_cs);
+        }
+        __syncthreads();
     }
 }
 
@@ -153,9 +177,19 @@ hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st) {
 }
 
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st) {
-    const int blocks = elementwise_blocks((int64_t)g.batch * g.M * g.N);
+    const int64_t plane = (int64_t)g.batch * g.M * g.N;
+    // threads per output: enough that a block covers ~8 planes per thread
+    const int tpo = g.splits >= 64 ? 8 : (g.splits >= 16 ? 4 : (g.splits >= 4 ? 2 : 1));
+    const int64_t opb = 256 / tpo;
+    int64_t blocks = (plane + opb - 1) / opb;
+    if (blocks > 8192) blocks = 8192;
     return with_dtype(dt, [&]<class T>() {
-        hipLaunchKernelGGL(k_splitk_reduce<T>, dim3(blocks), dim3(256), 0, st, g);
+        switch (tpo) {
+            case 8: hipLaunchKernelGGL((k_splitk_reduce<T, 8>), dim3(blocks), dim3(256), 0, st, g); break;
+            case 4: hipLaunchKernelGGL((k_splitk_reduce<T, 4>), dim3(blocks), dim3(256), 0, st, g); break;
+            case 2: hipLaunchKernelGGL((k_splitk_reduce<T, 2>), dim3(blocks), dim3(256), 0, st, g); break;
+            default: hipLaunchKernelGGL((k_splitk_reduce<T, 1>), dim3(blocks), dim3(256), 0, st, g); break;
+        }
         return hipGetLastError();
     });
 }

@@ -69,6 +69,8 @@ struct GemvArgs {
     int32_t epilogue, beta_nz, alpha_nz;
     int32_t vec_ok;
     int32_t splits, k_chunk;
+    int32_t grid_cap;   // persistent kernels: at most this many workgroups (0 = no cap)
+    int32_t x_row;      // dot family: X stored with its nv values contiguous per k
     EpiScalars s;
 };
 
@@ -86,6 +88,13 @@ int gemv_nv_bucket(int nv);   // template NV used for a given number of vectors
 hipError_t launch_gemv_dot(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_gemv_axpy(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 int gemv_axpy_vec(int dt, int nv);   // elements per lane of the vector path
+
+// gemv_fast.hip: streaming float kernels (16-byte aligned operands, K or rows multiple of
+// the 16-byte vector width)
+bool gemv_fast_dtype(int dt);
+int gemv_fast_vec(int dt);
+hipError_t launch_gemv_dot_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
+hipError_t launch_gemv_axpy_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 
 // gemm_mfma.hip
 struct MfmaTile {

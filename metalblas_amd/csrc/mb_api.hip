@@ -47,6 +47,7 @@ struct Plan {
     // GEMV
     GemvArgs gv;
     bool gemv_dot = false;
+    bool gemv_fast = false;   // streaming float kernels of gemv_fast.hip
     // MFMA / generic
     GemmArgs gg;
     MfmaTile tile = {0, 0, 0, 0};
@@ -214,15 +215,33 @@ bool plan_gemv(const Prob &p, Plan &pl) {
     g.s = p.s;
     g.splits = 1;
     g.k_chunk = g.K;
+    g.grid_cap = 2 * dev_info().cus;
     const bool batched = p.batch > 1;
+    bool fast = false;
     if (dot) {
         const int V = 16 / es;
-        bool ok = aligned(g.mat, 16) && (g.mat_ld * es) % 16 == 0 && (!batched || (g.mat_bs * es) % 16 == 0);
-        ok = ok && (g.K % V) == 0 && g.x_ks == 1 && aligned(g.x, 16) && (!batched || (g.x_bs * es) % 16 == 0);
+        const bool mat_ok =
+            aligned(g.mat, 16) && (g.mat_ld * es) % 16 == 0 && (!batched || (g.mat_bs * es) % 16 == 0) && (g.K % V) == 0;
+        bool ok = mat_ok && g.x_ks == 1 && aligned(g.x, 16) && (!batched || (g.x_bs * es) % 16 == 0);
         ok = ok && (nv == 1 || (g.x_vs * es) % 16 == 0);
         g.vec_ok = ok;
+        fast = ok && gemv_fast_dtype(p.dt);
+        // X with its nv values contiguous per k (row-major thin X): exact power-of-two nv,
+        // every k-row aligned to nv elements
+        const int bucket = gemv_nv_bucket((int)nv);
+        if (!fast && mat_ok && gemv_fast_dtype(p.dt) && nv > 1 && bucket == nv && g.x_vs == 1 &&
+            g.x_ks % nv == 0 && aligned(g.x, (int)nv * es) && (!batched || g.x_bs % nv == 0)) {
+            fast = true;
+            g.x_row = 1;
+        }
     } else {
-        const int V = gemv_axpy_vec(p.dt, (int)nv);
+        int V = gemv_axpy_vec(p.dt, (int)nv);
+        if (gemv_fast_dtype(p.dt)) {
+            const int Vf = gemv_fast_vec(p.dt);
+            fast = aligned(g.mat, 16) && (g.mat_ld * es) % 16 == 0 && (!batched || (g.mat_bs * es) % 16 == 0) &&
+                   (g.rows % Vf) == 0;
+            if (fast) V = Vf;
+        }
         const int vb = V * es;
         bool ok = aligned(g.mat, vb) && (g.mat_ld * es) % vb == 0 && (!batched || (g.mat_bs * es) % vb == 0);
         ok = ok && (g.rows % V) == 0;
@@ -246,6 +265,7 @@ bool plan_gemv(const Prob &p, Plan &pl) {
     }
     pl.family = dot ? MB_FAMILY_GEMV_DOT : MB_FAMILY_GEMV_AXPY;
     pl.gemv_dot = dot;
+    pl.gemv_fast = fast;
     pl.gv = g;
     return true;
 }
@@ -310,6 +330,33 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
                         p.tile[1] > 0;
     if (forced) {
         t = snap_tile(p.dt, p.tile, p.backend);
+    } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16) {
+        // Occupancy-aware cost model over the LDS-direct 16-bit tiles.  occ = workgroups per
+        // CU (LDS and VGPR limited), eff = relative per-CU throughput at that occupancy,
+        // measured on a bf16 8192^3 product on MI355X.  Time ~ rounds * occ * BM*BN / eff.
+        struct Cand {
+            MfmaTile t;
+            int occ;
+            double eff;
+        };
+        static const Cand cands[] = {
+            {{256, 256, 2, 4}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.91}, {{256, 128, 2, 2}, 1, 0.79},
+            {{128, 256, 2, 2}, 1, 0.73}, {{128, 128, 2, 2}, 1, 0.52}, {{128, 64, 2, 2}, 2, 0.62},
+            {{64, 128, 2, 2}, 2, 0.70},  {{64, 64, 2, 2}, 3, 0.59},
+        };
+        double best = 1e300;
+        t = {64, 64, 2, 2};
+        for (const auto &c : cands) {
+            const int64_t tiles = ((p.M + c.t.bm - 1) / c.t.bm) * ((p.N + c.t.bn - 1) / c.t.bn) * p.batch;
+            const int64_t slots = (int64_t)cus * c.occ;
+            const int64_t rounds = (tiles + slots - 1) / slots;
+            const int64_t per_cu = tiles < cus ? 1 : (c.occ < (tiles + cus - 1) / cus ? c.occ : (tiles + cus - 1) / cus);
+            const double cost = (double)rounds * per_cu * c.t.bm * c.t.bn / c.eff;
+            if (cost < best * 0.999) {
+                best = cost;
+                t = c.t;
+            }
+        }
     } else {
         static const MfmaTile order[] = {{256, 256, 2, 2}, {256, 128, 2, 2}, {128, 256, 2, 2},
                                          {128, 128, 2, 2}, {128, 64, 2, 2},  {64, 128, 2, 2},
@@ -453,12 +500,13 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
             break;
         }
         case MB_FAMILY_GEMV_DOT:
-            e = launch_gemv_dot(pl.p.dt, pl.gv, st, shape);
+            e = pl.gemv_fast ? launch_gemv_dot_fast(pl.p.dt, pl.gv, st, shape)
+                             : launch_gemv_dot(pl.p.dt, pl.gv, st, shape);
             break;
         case MB_FAMILY_GEMV_AXPY: {
             GemvArgs &g = pl.gv;
             g.ws = d->workspace;
-            e = launch_gemv_axpy(pl.p.dt, g, st, shape);
+            e = pl.gemv_fast ? launch_gemv_axpy_fast(pl.p.dt, g, st, shape) : launch_gemv_axpy(pl.p.dt, g, st, shape);
             if (e == hipSuccess && g.splits > 1) {
                 // sum the K slices: partial planes are [split][batch][nv][rows]
                 GemmArgs r;
@@ -548,6 +596,7 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
     } else if (pl.family == MB_FAMILY_GEMV_DOT || pl.family == MB_FAMILY_GEMV_AXPY) {
         info->tile[0] = pl.gv.nv;
         info->tile[1] = pl.gv.vec_ok;
+        info->tile[2] = pl.gemv_fast;
         info->split_k = pl.gv.splits;
         info->block = 256;
     }

@@ -311,3 +311,63 @@ def test_empty_and_k0(dev):
     bias = torch.randn(5, device=dev)
     r = mb.addmm(bias, torch.randn(4, 0, device=dev), torch.randn(0, 5, device=dev), beta=2.0)
     assert torch.allclose(r, (2.0 * bias).expand(4, 5))
+
+
+# ---- thin products: every GEMV family, both operand layouts, 1..16 vectors --------------------
+
+THIN_NV = [1, 2, 3, 5, 8, 12, 16]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8,
+                                   torch.int32, torch.complex64], ids=str)
+@pytest.mark.parametrize("nv", THIN_NV)
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+def test_thin_n(dev, dtype, nv, layout):
+    """W @ X with a thin X (N = nv): W row/col-major, X row/col-major."""
+    g = gen(nv)
+    M, K = 1024, 2048
+    a = rand((M, K), dtype, g) if layout[0] == "r" else rand((K, M), dtype, g).t()
+    b = rand((K, nv), dtype, g) if layout[1] == "r" else rand((nv, K), dtype, g).t()
+    got = mb.matmul(_to(a, dev), _to(b, dev))
+    assert_parity(got, a, b, tag=f"thin-N {dtype} nv={nv} {layout}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8,
+                                   torch.int32, torch.complex64], ids=str)
+@pytest.mark.parametrize("nv", THIN_NV)
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+def test_thin_m(dev, dtype, nv, layout):
+    """X @ W with a thin X (M = nv)."""
+    g = gen(100 + nv)
+    N, K = 1024, 2048
+    a = rand((nv, K), dtype, g) if layout[0] == "r" else rand((K, nv), dtype, g).t()
+    b = rand((K, N), dtype, g) if layout[1] == "r" else rand((N, K), dtype, g).t()
+    got = mb.matmul(_to(a, dev), _to(b, dev))
+    assert_parity(got, a, b, tag=f"thin-M {dtype} nv={nv} {layout}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("shape", [(4096, 8, 4096), (8, 4096, 4096), (3000, 1, 2048), (1, 3000, 2048)], ids=str)
+def test_thin_addmm(dev, dtype, shape):
+    M, N, K = shape
+    g = gen(7)
+    a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    bias = rand((N,), dtype, g)
+    got = mb.addmm(bias.to(dev), a.to(dev), b.to(dev), beta=0.5, alpha=2.0)
+    assert_parity(got, a, b, bias=bias, beta=0.5, alpha=2.0, tag=f"thin addmm {dtype} {shape}")
+
+
+@pytest.mark.parametrize("n", [8192, 16384])
+def test_gemv_config2_sizes(dev, n):
+    """BASELINE config 2 at full size: y = W @ x, x @ W and 8-vector thin products,
+    checked on sampled rows against the oracle."""
+    g = gen(1)
+    W = torch.randn(n, n, generator=g).to(torch.bfloat16)
+    x = torch.randn(n, generator=g).to(torch.bfloat16)
+    Wd, xd = W.to(dev), x.to(dev)
+    assert_parity(mb.matmul(Wd, xd).reshape(n, 1), W, x.reshape(n, 1), tag="W@x")
+    assert_parity(mb.matmul(xd, Wd).reshape(1, n), x.reshape(1, n), W, tag="x@W")
+    X8 = torch.randn(8, n, generator=g).to(torch.bfloat16)
+    assert_parity(mb.matmul(X8.to(dev), Wd), X8, W, tag="X8@W")
+    Xn = torch.randn(n, 8, generator=g).to(torch.bfloat16)
+    assert_parity(mb.matmul(Wd, Xn.to(dev)), W, Xn, tag="W@X8")
