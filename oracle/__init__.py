@@ -5,8 +5,9 @@ cpu_baseline leg, never by the metalblas_amd package.
 
 ``gemm(a, b, ...)`` runs the C restatement on CPU tensors of any strides and returns
 ``(c, exact)``: ``c`` in the input dtype (rounded / wrapped exactly as the reference
-specifies) and ``exact`` as float64 / complex128 / int64 (pre-rounding value; for integers
-the wrapped result).  The descriptor layout mirrors include/metalblas_amd.h and is defined
+specifies) and ``exact`` as float64 / complex128 / int64 (the value before the final rounding; for
+integers the 64-bit wraparound accumulator before truncation to the output width, carried
+through a double and so exact only below 2^53).  The descriptor layout mirrors include/metalblas_amd.h and is defined
 here independently of the product's own binding.
 """
 from __future__ import annotations

@@ -1,0 +1,320 @@
+"""CPU tests of the host side: the C ABI's exports and struct layout, the planner's decisions
+for the BASELINE configurations, error mapping, and the Python layout/scalar logic of
+metalblas/dispatch.py that the drop-in keeps.  Nothing here launches a kernel."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+import metalblas_amd as mb
+from metalblas_amd import _lib, dispatch, planner
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "metalblas_amd.h")
+
+
+def _declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[\w\s\*]+?\b(mb_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared_functions()
+    assert {"mb_gemm", "mb_plan", "mb_query", "mb_strerror"} <= set(names)
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/metalblas_amd.h but not exported"
+    assert set(names) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def _c_layout():
+    """sizeof/offsetof of the ABI structs, as the C compiler lays them out."""
+    fields = {
+        "mb_matrix": [f for f, _ in _lib.MbMatrix._fields_],
+        "mb_gemm_desc": [f for f, _ in _lib.MbGemmDesc._fields_],
+        "mb_plan_info": [f for f, _ in _lib.MbPlanInfo._fields_],
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void) {"]
+    for s, fs in fields.items():
+        lines.append(f'printf("{s} size %zu\\n", sizeof({s}));')
+        for f in fs:
+            lines.append(f'printf("{s} {f} %zu\\n", offsetof({s}, {f}));')
+    lines.append("return 0; }")
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-std=c11", "-o", exe, src], check=True)
+        out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    res = {}
+    for ln in out.splitlines():
+        s, f, v = ln.split()
+        res[(s, f)] = int(v)
+    return res
+
+
+def test_ctypes_layout_matches_header():
+    import oracle
+    c = _c_layout()
+    for s, cls in (("mb_matrix", _lib.MbMatrix), ("mb_gemm_desc", _lib.MbGemmDesc),
+                   ("mb_plan_info", _lib.MbPlanInfo)):
+        assert ctypes.sizeof(cls) == c[(s, "size")], s
+        for f, _ in cls._fields_:
+            assert getattr(cls, f).offset == c[(s, f)], f"{s}.{f}"
+    # the oracle binds the same descriptor independently
+    assert ctypes.sizeof(oracle.Desc) == c[("mb_gemm_desc", "size")]
+    for f, _ in oracle.Desc._fields_:
+        assert getattr(oracle.Desc, f).offset == c[("mb_gemm_desc", f)]
+
+
+def test_strerror_and_status_mapping():
+    for code in range(0, -9, -1):
+        assert _lib.strerror(code) != "unknown status"
+    assert _lib.strerror(-99) == "unknown status"
+    _lib.check(0)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_GEMV_SHAPE)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_BAD_BACKEND)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.ERR_UNSUPPORTED_DTYPE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_LAUNCH)
+
+
+def _desc(dtype, a, b, c=None, batch=1, **kw):
+    """Descriptor of CPU tensors (for planning only: nothing is launched)."""
+    if c is None:
+        shape = (a.shape[0], a.shape[1], b.shape[2]) if a.dim() == 3 else (a.shape[0], b.shape[1])
+        c = torch.empty(shape, dtype=dtype)
+    if a.dim() == 3:
+        batch, M, K = a.shape
+        N = b.shape[2]
+    else:
+        M, K = a.shape
+        N = b.shape[1]
+    return _lib.make_desc(dtype, batch, M, N, K, dispatch._mat(a), dispatch._mat(b), dispatch._mat(c), **kw)
+
+
+def _plan(dtype, a, b, **kw):
+    return _lib.plan(_desc(dtype, a, b, **kw))
+
+
+def test_abi_rejects_bad_descriptors_before_launch():
+    lib = _lib.load()
+    a = torch.empty(8, 8, dtype=torch.float32)
+    d = _desc(torch.float32, a, a)
+    d.dtype = 42
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_UNSUPPORTED_DTYPE
+    d = _desc(torch.float32, a, a, backend=_lib.BACKEND_GEMV)
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_GEMV_SHAPE
+    d = _desc(torch.float32, a, a)
+    d.backend = 17
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_BAD_BACKEND
+    d = _desc(torch.float32, a, a)
+    d.flags = 1
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    d = _desc(torch.float32, a, a)
+    d.M = -1
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    d = _desc(torch.float32, a, a)
+    d.c.ptr = None
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    # an epilogue that reads the bias needs one
+    d = _desc(torch.float32, a, a, epilogue=(1.0, 1.0, True, True))
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    # empty outputs are a successful no-op
+    e = torch.empty(0, 8)
+    d = _desc(torch.float32, e, a, c=torch.empty(0, 8))
+    assert lib.mb_gemm(ctypes.byref(d), None) == 0
+
+
+# ---- planner decisions at the BASELINE configurations (256 CUs assumed without a GPU) ---------
+
+def test_plan_config3_square_bf16_uses_matrix_cores():
+    a = torch.empty(8192, 8192, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, a, a)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k == 1 and p.workspace_bytes == 0
+    assert p.tile[0] * p.tile[1] >= 128 * 128
+
+
+@pytest.mark.parametrize("layout", ["rm_rm", "rm_cm", "cm_rm", "cm_cm", "row_sliced"])
+def test_plan_config3_layouts_use_matrix_cores(layout):
+    M, K, N = 2048, 4096, 2048
+    a = torch.empty(K, M, dtype=torch.bfloat16).t() if layout.startswith("cm") else \
+        torch.empty(2 * M, K, dtype=torch.bfloat16)[::2] if layout == "row_sliced" else \
+        torch.empty(M, K, dtype=torch.bfloat16)
+    b = torch.empty(N, K, dtype=torch.bfloat16).t() if layout.endswith("cm") else torch.empty(K, N, dtype=torch.bfloat16)
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, a, b).family] == "mfma"
+
+
+def test_plan_config2_gemv_families():
+    n = 16384
+    W = torch.empty(n, n, dtype=torch.bfloat16)
+    x = torch.empty(n, 1, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, W, x)
+    assert _lib.FAMILY_NAMES[p.family] == "gemv_dot" and p.tile[2] == 1   # streaming kernel
+    xt = torch.empty(1, n, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, xt, W)
+    assert _lib.FAMILY_NAMES[p.family] == "gemv_axpy" and p.tile[2] == 1
+    # x @ W streams W along its rows: split over K to fill 256 CUs, partials in the workspace
+    assert p.split_k > 1 and p.workspace_bytes == p.split_k * n * 4
+    X8 = torch.empty(8, n, dtype=torch.bfloat16)
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, X8, W).family] == "gemv_axpy"
+    Xn = torch.empty(n, 8, dtype=torch.bfloat16)
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, W, Xn).family] == "gemv_dot"
+
+
+def test_plan_config4_splitk_and_batches():
+    a = torch.empty(1, 128, 65536, dtype=torch.float16)
+    b = torch.empty(1, 65536, 128, dtype=torch.float16)
+    p = _plan(torch.float16, a, b)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k > 1
+    assert p.workspace_bytes == p.split_k * 128 * 128 * 4
+    a = torch.empty(8, 512, 256, dtype=torch.float16)
+    b = torch.empty(8, 256, 512, dtype=torch.float16)
+    assert _lib.FAMILY_NAMES[_plan(torch.float16, a, b).family] == "mfma"
+    bb = torch.empty(256, 512, dtype=torch.float16).expand(8, 256, 512)   # stride-0 batch
+    assert _lib.FAMILY_NAMES[_plan(torch.float16, a, bb).family] == "mfma"
+
+
+def test_plan_config5_int8_and_complex():
+    a = torch.empty(4096, 4096, dtype=torch.int8)
+    assert _lib.FAMILY_NAMES[_plan(torch.int8, a, a).family] == "mfma"
+    A = torch.empty(8192, 8192, dtype=torch.complex64)
+    x = torch.empty(8192, 1, dtype=torch.complex64)
+    assert _lib.FAMILY_NAMES[_plan(torch.complex64, A, x).family] == "gemv_dot"
+
+
+def test_plan_k0_fill_and_empty():
+    a = torch.empty(4, 0, dtype=torch.bfloat16)
+    b = torch.empty(0, 5, dtype=torch.bfloat16)
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, a, b).family] == "fill"
+    a = torch.empty(0, 3, dtype=torch.bfloat16)
+    b = torch.empty(3, 5, dtype=torch.bfloat16)
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, a, b).family] == "none"
+
+
+def test_plan_column_major_output_is_transposed_problem():
+    a = torch.empty(256, 512, dtype=torch.bfloat16)
+    b = torch.empty(512, 384, dtype=torch.bfloat16)
+    c = torch.empty(384, 256, dtype=torch.bfloat16).t()
+    p = _lib.plan(_desc(torch.bfloat16, a, b, c=c))
+    assert p.transposed == 1
+
+
+def test_tile_candidates_primary_first():
+    a = torch.empty(4096, 4096, dtype=torch.bfloat16)
+    d = _desc(torch.bfloat16, a, a)
+    p = _lib.plan(d)
+    cands = _lib.tile_candidates(d)
+    assert len(cands) >= 2 and cands[0][:2] == tuple(p.tile[:2])
+    assert len(set(c[:5] for c in cands)) == len(cands)
+
+
+# ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
+
+def test_unit_lead_classification():
+    """metalblas/dispatch.py:23-35 on the BASELINE config-3 layouts."""
+    M, K = 64, 96
+    rm = torch.empty(M, K)
+    assert dispatch._unit_lead(rm, M, K) == (False, K)
+    cm = torch.empty(K, M).t()
+    assert dispatch._unit_lead(cm, M, K) == (True, M)
+    rows = torch.empty(2 * M, K)[::2]
+    assert dispatch._unit_lead(rows, M, K) == (False, 2 * K)
+    cols = torch.empty(M, 2 * K)[:, ::2]
+    assert dispatch._unit_lead(cols, M, K) is None
+    assert dispatch._matrix_view(cols, M, K).is_contiguous()
+    off = torch.empty(M * K + 17)[17:].view(M, K)
+    assert dispatch._unit_lead(off, M, K) == (False, K) and off.storage_offset() == 17
+    assert dispatch._matrix_view(off, M, K).data_ptr() == off.data_ptr()   # no copy
+
+
+def test_scalars_cast_like_reference():
+    """metalblas/dispatch.py:127-131."""
+    assert dispatch._scalars(torch.int32, 2.7, -1.2) == (2, -1, True, True)
+    assert dispatch._scalars(torch.int8, 0.4, 1) == (0, 1, False, True)
+    assert dispatch._scalars(torch.bfloat16, 1, 0) == (1.0, 0.0, True, False)
+    beta, alpha, bnz, anz = dispatch._scalars(torch.complex64, 1j, 0)
+    assert beta == 1j and alpha == 0 and bnz and not anz
+
+
+def test_make_desc_fields():
+    a = torch.empty(4 * 6 + 17)[17:].view(4, 6)
+    b = torch.empty(5, 6).t()
+    c = torch.empty(4, 5)
+    d = _lib.make_desc(torch.float32, 1, 4, 5, 6, dispatch._mat(a), dispatch._mat(b), dispatch._mat(c),
+                       epilogue=(0.5, -2, True, True), swizzle_log=2)
+    assert d.a.ptr == a.data_ptr() and (d.a.row_stride, d.a.col_stride) == (6, 1)
+    assert (d.b.row_stride, d.b.col_stride) == (1, 6)
+    assert d.epilogue == 1 and d.beta_re == 0.5 and d.alpha_re == -2.0 and d.alpha_int == -2
+    assert d.swizzle_log == 2
+    assert _lib._wrap64(2 ** 64 - 1) == -1 and _lib._wrap64(-5) == -5
+
+
+@pytest.mark.parametrize("op", ["matmul", "bmm", "addmm"])
+def test_cpu_tensors_are_rejected(op):
+    """The reference asserts its device (metalblas/dispatch.py:118,191); so does the drop-in:
+    no silent CPU fallback."""
+    a = torch.randn(4, 4)
+    with pytest.raises(AssertionError):
+        if op == "matmul":
+            mb.matmul(a, a)
+        elif op == "bmm":
+            mb.bmm(a[None], a[None])
+        else:
+            mb.addmm(a, a, a)
+
+
+def test_api_surface_matches_reference():
+    """metalblas/__init__.py exports these names."""
+    for name in ("matmul", "gemm", "addmm", "bmm", "baddbmm", "addbmm", "dot", "vdot", "outer",
+                 "ger", "mv", "kernels"):
+        assert hasattr(mb, name)
+    assert mb.gemm is mb.matmul and mb.ger is mb.outer
+    assert callable(mb.kernels.has_metal4)
+    for bk in ("gemv", "mpp_tensor", "mpp", "simd", "auto", None):
+        assert bk in dispatch.BACKENDS
+
+
+def test_autotune_probe_params_and_cache(tmp_path, monkeypatch):
+    w0 = planner.probe_params(256, 256, 256)
+    w2 = planner.probe_params(8192, 8192, 8192)
+    assert w0[1] >= w2[1] and w0[0] >= w2[0]
+    path = tmp_path / "plans.json"
+    monkeypatch.setattr(planner, "_CACHE_PATH", str(path))
+    planner.clear()
+    planner._PLANS["k1"] = (256, 256, 64, 2, 4, 0, 0, 0)
+    planner._PLANS["k2"] = None
+    planner._save_cache()
+    saved = json.loads(path.read_text())
+    assert saved["k1"][:2] == [256, 256] and saved["k2"] is None
+    planner.clear()
+    monkeypatch.setattr(planner, "_loaded", False)
+    planner._load_cache()
+    assert planner.cached()["k1"][:2] == (256, 256)
+    planner.clear()
+
+
+def test_autotune_switch(monkeypatch):
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "0")
+    assert not planner.enabled()
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
+    assert planner.enabled()
+
+
+def test_product_never_touches_the_oracle():
+    """The oracle is test infrastructure: the package must not import, load or run it."""
+    pkg = os.path.join(ROOT, "metalblas_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".hpp", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f
+                assert "mb_oracle" not in text and "libmb_oracle" not in text, f
