@@ -33,7 +33,9 @@ def parse():
     p.add_argument("--size", type=int, default=8192)
     p.add_argument("--gemv", type=int, default=16384)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    p.add_argument("--only", choices=["all", "gemm", "gemv"], default="all")
+    p.add_argument("--only", choices=["all", "gemm", "gemv", "copy"], default="all",
+                   help="copy: a plain 1 GiB device copy, the calibration run for HBM counters")
+    p.add_argument("--no-tune", action="store_true", help="static plans only (METALBLAS_AUTOTUNE=0)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     return p.parse_args()
 
@@ -126,8 +128,20 @@ def main():
         print(json.dumps({"error": "this build measures one GPU only (--gpus 1); the multi-GPU "
                           "sharding is a design in DESIGN.md, not a measured path"}))
         sys.exit(2)
+    if args.no_tune:
+        os.environ["METALBLAS_AUTOTUNE"] = "0"
     import torch
     import metalblas_amd as mb
+    if args.only == "copy":
+        nbytes = 1 << 30
+        src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup):
+            dst.copy_(src)
+        ms = time_events(lambda: dst.copy_(src), args.steps)
+        print(json.dumps({"copy_bytes_each_way": nbytes, "ms": round(ms, 4),
+                          "GBps_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}))
+        return
 
     result = {
         "metric": "TFLOP/s + % MFMA peak (bf16 GEMM 8192³); GEMV HBM GB/s + % peak",

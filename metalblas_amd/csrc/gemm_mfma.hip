@@ -17,29 +17,32 @@ hipError_t launch_bf16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, di
 hipError_t launch_bf16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_f16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_f16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_bf16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_f16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
 }  // namespace m16
 
 namespace {
 // ---- compiled tile table ----------------------------------------------------------------
 struct TileEntry {
-    int bm, bn, wm, wn;
+    int bm, bn, wm, wn, sched;
 };
 // register-staged family (mfma_gemm.hpp): every matrix-core dtype
 constexpr TileEntry kTiles[] = {
-    {256, 256, 2, 2}, {256, 128, 2, 2}, {128, 256, 2, 2}, {128, 128, 2, 2},
-    {128, 64, 2, 2},  {64, 128, 2, 2},  {64, 64, 2, 2},   {32, 32, 1, 1},
+    {256, 256, 2, 2, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0}, {128, 128, 2, 2, 0},
+    {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},   {32, 32, 1, 1, 0},
 };
-// LDS-direct 16-bit family (mfma16.hpp): bf16 / fp16
+// LDS-direct 16-bit family (mfma16.hpp): bf16 / fp16; sched 1 = the ping-pong kernel
 constexpr TileEntry kTiles16[] = {
-    {256, 256, 2, 2}, {256, 256, 2, 4}, {256, 128, 2, 2}, {128, 256, 2, 2},
-    {128, 128, 2, 2}, {128, 64, 2, 2},  {64, 128, 2, 2},  {64, 64, 2, 2},  {32, 32, 1, 1},
+    {256, 256, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
+    {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
 };
 
 bool is16(int dt) { return dt == BF16 || dt == F16; }
 
 bool in_table(const TileEntry *tb, int n, const MfmaTile &t) {
     for (int i = 0; i < n; ++i)
-        if (tb[i].bm == t.bm && tb[i].bn == t.bn && tb[i].wm == t.wm && tb[i].wn == t.wn) return true;
+        if (tb[i].bm == t.bm && tb[i].bn == t.bn && tb[i].wm == t.wm && tb[i].wn == t.wn && tb[i].sched == t.sched)
+            return true;
     return false;
 }
 
@@ -70,7 +73,7 @@ int mfma_list_tiles(int dt, MfmaTile *out, int cap) {
     const int cnt = is16(dt) ? (int)(sizeof(kTiles16) / sizeof(kTiles16[0])) : (int)(sizeof(kTiles) / sizeof(kTiles[0]));
     int n = 0;
     for (int i = 0; i < cnt; ++i) {
-        if (n < cap) out[n] = {tb[i].bm, tb[i].bn, tb[i].wm, tb[i].wn};
+        if (n < cap) out[n] = {tb[i].bm, tb[i].bn, tb[i].wm, tb[i].wn, tb[i].sched};
         ++n;
     }
     return n;
@@ -84,6 +87,9 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
     if (is16(dt) && !(t.bm == 32 && t.bn == 32)) {
         if (m16_offsets_fit(t, a_kc, b_kc, g)) {
             const bool whole = (g.k_chunk % 64) == 0 && (g.K % 64) == 0;
+            if (t.sched == 1)
+                return dt == BF16 ? m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st)
+                                  : m16::launch_f16_pp(!whole, a_kc, b_kc, g, grid, st);
             if (dt == BF16)
                 return whole ? m16::launch_bf16_kwhole(t, a_kc, b_kc, g, grid, st)
                              : m16::launch_bf16_ktail(t, a_kc, b_kc, g, grid, st);
@@ -91,7 +97,7 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
                          : m16::launch_f16_ktail(t, a_kc, b_kc, g, grid, st);
         }
         // very large leading dimensions: register-staged kernel with a compiled 4-wave tile
-        MfmaTile v = in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t) ? t : MfmaTile{128, 128, 2, 2};
+        MfmaTile v = in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t) ? t : MfmaTile{128, 128, 2, 2, 0};
         dim3 grid2(cdiv(g.M, v.bm) * cdiv(g.N, v.bn), g.splits, grid.z);
         if (shape) *shape = {grid2, dim3(64 * v.wm * v.wn)};
         return dt == BF16 ? mfma::launch_bf16(v, a_kc, b_kc, g, grid2, st) : mfma::launch_f16(v, a_kc, b_kc, g, grid2, st);

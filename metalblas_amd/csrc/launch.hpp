@@ -99,6 +99,7 @@ hipError_t launch_gemv_axpy_fast(int dt, const GemvArgs &g, hipStream_t st, Laun
 // gemm_mfma.hip
 struct MfmaTile {
     int bm, bn, wm, wn;   // block tile and wave grid
+    int sched = 0;        // 0: interleaved LDS reads / MFMAs per wave; 1: two-group ping-pong
 };
 bool mfma_supported_dtype(int dt);
 int mfma_k_align(int dt);   // elements per 16-byte chunk along K

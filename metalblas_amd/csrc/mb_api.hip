@@ -271,12 +271,17 @@ bool plan_gemv(const Prob &p, Plan &pl) {
 }
 
 // ---- matrix-core planning ---------------------------------------------------------------
-MfmaTile snap_tile(int dt, const int32_t *t, int backend) {
+// The compiled tile nearest to a requested one.  tile = (BM, BN, BK, WM, WN, schedule + 1):
+// an explicit wave grid (WM, WN) and schedule are honoured when compiled; BK is fixed by the
+// dtype.  The reference's (BM, BN, NSG) form for backend="mpp_tensor" leaves WM/WN at 0 and
+// gets the default 2 x 2 wave grid.
+MfmaTile snap_tile(int dt, const int32_t *t) {
     MfmaTile want = {t[0], t[1], 2, 2};
-    if (backend == MB_BACKEND_TILED && t[3] > 0 && t[4] > 0) {
+    if (t[3] > 0 && t[4] > 0) {
         want.wm = t[3];
         want.wn = t[4];
     }
+    const int want_sched = t[5] > 0 ? t[5] - 1 : -1;
     MfmaTile list[32];
     const int n = mfma_list_tiles(dt, list, 32);
     int best = 0;
@@ -285,6 +290,7 @@ MfmaTile snap_tile(int dt, const int32_t *t, int backend) {
         double d = fabs(log2((double)list[i].bm / (want.bm > 0 ? want.bm : 1))) +
                    fabs(log2((double)list[i].bn / (want.bn > 0 ? want.bn : 1)));
         if (list[i].wm != want.wm || list[i].wn != want.wn) d += 0.01;
+        if (want_sched >= 0 && list[i].sched != want_sched) d += 0.005;
         if (d < bestd) {
             bestd = d;
             best = i;
@@ -326,10 +332,11 @@ bool mfma_layout_ok(const Prob &p, bool &a_kc, bool &b_kc) {
 void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const int cus = dev_info().cus;
     MfmaTile t;
-    const bool forced = (p.backend == MB_BACKEND_MATRIX || p.backend == MB_BACKEND_TILED) && p.tile[0] > 0 &&
-                        p.tile[1] > 0;
+    // a tile in the descriptor is honoured for the matrix-core backends and for AUTO (where
+    // the autotuner puts the tile it measured fastest)
+    const bool forced = p.tile[0] > 0 && p.tile[1] > 0;
     if (forced) {
-        t = snap_tile(p.dt, p.tile, p.backend);
+        t = snap_tile(p.dt, p.tile);
     } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16) {
         // Occupancy-aware cost model over the LDS-direct 16-bit tiles.  occ = workgroups per
         // CU (LDS and VGPR limited), eff = relative per-CU throughput at that occupancy,
@@ -340,7 +347,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
             double eff;
         };
         static const Cand cands[] = {
-            {{256, 256, 2, 4}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.91}, {{256, 128, 2, 2}, 1, 0.79},
+            {{256, 256, 2, 4, 1}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.91}, {{256, 128, 2, 2}, 1, 0.79},
             {{128, 256, 2, 2}, 1, 0.73}, {{128, 128, 2, 2}, 1, 0.52}, {{128, 64, 2, 2}, 2, 0.62},
             {{64, 128, 2, 2}, 2, 0.70},  {{64, 64, 2, 2}, 3, 0.59},
         };
@@ -579,8 +586,9 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
         info->tile[2] = 8 * (16 / dtype_size(pl.p.dt));
         info->tile[3] = pl.tile.wm;
         info->tile[4] = pl.tile.wn;
-        info->tile[5] = pl.a_kc;
-        info->tile[6] = pl.b_kc;
+        info->tile[5] = pl.tile.sched + 1;
+        info->tile[6] = pl.a_kc;
+        info->tile[7] = pl.b_kc;
         info->split_k = pl.gg.splits;
         info->swizzle_log = pl.gg.swz;
         info->block = 64 * pl.tile.wm * pl.tile.wn;
@@ -616,13 +624,16 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
             int32_t *q = tiles + 8 * out;
             memset(q, 0, 8 * sizeof(int32_t));
             q[0] = t.bm; q[1] = t.bn; q[2] = 8 * (16 / dtype_size(pl.p.dt)); q[3] = t.wm; q[4] = t.wn;
+            q[5] = t.sched + 1;
         }
         ++out;
     };
     emit(pl.tile);
     for (int i = 0; i < n && i < 32; ++i) {
         const MfmaTile &t = list[i];
-        if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn) continue;
+        if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn &&
+            t.sched == pl.tile.sched)
+            continue;
         if (t.bm > 2 * pl.p.M + 32 || t.bn > 2 * pl.p.N + 32) continue;
         emit(t);
     }

@@ -35,10 +35,66 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 #define MB_LDS __attribute__((address_space(3)))
 
-__device__ void raw_buffer_load_lds(i32x4 rsrc, MB_LDS uint32_t *lds, int size, int voffset, int soffset,
-                                    int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
-
 constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that is always out of range
+
+// One LDS-direct load: 64 lanes x 16 bytes from rsrc + voffset + soffset into LDS at lds_addr
+// (+ 16 * lane), written as inline assembly.  The compiler does not model the LDS write of an
+// asm statement, so it adds no wait of its own before later LDS reads; with the intrinsic
+// form it waits for EVERY outstanding LDS-direct load before the first LDS read of a stage,
+// which exposes the whole global-load latency of the prefetched stage once per stage.  The
+// kernel instead waits for its own loads right before the barrier that publishes a stage,
+// when only that stage's loads (and one L2 prefetch) are in flight.  M0 carries the LDS
+// address; the s_nop covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset, int soffset) {
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
+                 : "memory");
+}
+__device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// All but the most recent load have completed (loads retire in issue order).
+__device__ __forceinline__ void vm_wait_but_one() { asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); }
+
+// L2 prefetch of one 128-byte line per lane: a dword LDS-direct load into a junk LDS area, so
+// no VGPR is written behind the compiler's back.  Out-of-range offsets load nothing.
+__device__ __forceinline__ void pf_line(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset, int soffset) {
+    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+                 :
+                 : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
+                 : "memory");
+}
+constexpr int kPfDist = 3;   // stages between a line's L2 prefetch and its LDS-direct load
+
+// Byte offset (from the operand tile's first element) of 128-byte line `idx` of one 64-deep
+// stage of a ROWS-wide operand tile, or kOOB.  K-contiguous operands have one line per row;
+// M/N-contiguous ones have ROWS * 2 / 128 lines per k.  Every stage has ROWS lines.
+template <int ROWS, bool KC>
+__device__ __forceinline__ uint32_t pf_line_offset(int idx, int64_t ld, int rows_left, int k_left) {
+    if constexpr (KC) {
+        if (idx >= ROWS || idx >= rows_left) return kOOB;
+        return (uint32_t)((int64_t)idx * ld * 2);
+    } else {
+        constexpr int LPR = ROWS * 2 / 128;
+        const int r = idx / LPR, c = idx % LPR;
+        if (r >= 64 || r >= k_left || c * 64 >= rows_left) return kOOB;
+        return (uint32_t)(((int64_t)r * ld + c * 64) * 2);
+    }
+}
+// XCD-cooperative prefetch assignment.  The tiles that run together on one XCD form an
+// 8 (M) x 4 (N) block (tile_coords16 order), so each A stage is shared by 4 workgroups and
+// each B stage by 8: workgroup (tm, tn) prefetches quarter (tn % 4) of its A lines with
+// wave 0 and eighth (tm % 8) of its B lines with wave 1.  The assignment only steers which
+// lines reach L2 early; every wave issues exactly one prefetch per stage so the vmcnt
+// arithmetic stays uniform.
+template <int BM, int BN, bool A_KC, bool B_KC>
+__device__ __forceinline__ uint32_t pf_assign(int wave, int lane, int tm, int tn, int64_t lda, int64_t ldb,
+                                              int rows_a, int rows_b, int k_left) {
+    if (wave == 0 && lane < BM / 4)
+        return pf_line_offset<BM, A_KC>((tn & 3) * (BM / 4) + lane, lda, rows_a, k_left);
+    if (wave == 1 && lane < BN / 8)
+        return pf_line_offset<BN, B_KC>((tm & 7) * (BN / 8) + lane, ldb, rows_b, k_left);
+    return kOOB;
+}
 
 struct __attribute__((packed)) BufRes {
     const void *base;
@@ -68,6 +124,9 @@ template <int CPR> __device__ __forceinline__ int swz_mn(int k) {
 }
 
 __device__ __forceinline__ MB_LDS char *lds_ptr(const char *p) { return (MB_LDS char *)(MB_LDS void *)p; }
+__device__ __forceinline__ uint32_t lds_addr(const char *p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_ptr(p));
+}
 
 // One operand tile: ROWS (M or N) x 64 k, 16-bit elements.
 template <int ROWS, int NW, bool KC> struct Tile16 {
@@ -152,6 +211,88 @@ __device__ __forceinline__ void tile_coords16(int pid, int tiles_m, int tiles_n,
     tn = in / gsz;
 }
 
+// Store a wave's accumulators: acc[i][j] holds the 32 x 32 block at rows mw + 32 j, columns
+// nw + 32 i; lane l owns row (l % 32) and columns 8 (r / 4) + 4 (l / 32) + r % 4 of register r.
+// Split-K slices write fp32 partial planes; otherwise the (optional) epilogue and one rounding.
+template <class T, int TM, int TN>
+__device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN][TM], int mw, int nw, int bz,
+                                             int ks, int lane) {
+    // keep the store addressing from being hoisted above the main loop (where its 64-bit
+    // addresses would be live across the loop and spill)
+    asm volatile("" : "+s"(mw), "+s"(nw));
+    const int mrow = lane & 31;
+    const int nsub = 4 * (lane >> 5);
+    T *Cb = (T *)g.c + bz * g.c_bs;
+    if (g.splits > 1) {
+        float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
+        const bool vec = (g.N & 3) == 0;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int gm = mw + j * 32 + mrow;
+                if (gm >= g.M) continue;
+                float *row = ws + (int64_t)gm * g.N;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int gn = nw + i * 32 + 8 * q + nsub;
+                    if (vec && gn + 3 < g.N) {
+                        *(float4 *)(row + gn) = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                            acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (gn + r < g.N) row[gn + r] = acc[i][j][4 * q + r];
+                    }
+                }
+            }
+    } else if (g.vec_ok && !g.epilogue) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int gm = mw + j * 32 + mrow;
+                if (gm >= g.M) continue;
+                T *row = Cb + gm * g.c_rs;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int gn = nw + i * 32 + 8 * q + nsub;
+                    if (gn + 3 < g.N) {
+                        T o[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
+                        uint2 u;
+                        __builtin_memcpy(&u, o, 8);
+                        *(uint2 *)(row + gn) = u;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (gn + r < g.N) row[gn + r] = (T)acc[i][j][4 * q + r];
+                    }
+                }
+            }
+    } else {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int gm = mw + j * 32 + mrow;
+                if (gm >= g.M) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int gn = nw + i * 32 + 8 * q + nsub;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int n = gn + r;
+                        if (n < g.N)
+                            store_out<T>(g, Cb + gm * g.c_rs + n * g.c_cs, acc[i][j][4 * q + r],
+                                         bz * g.bias_bs + gm * g.bias_rs + n * g.bias_cs);
+                    }
+                }
+            }
+    }
+}
+
 // KTAIL: some K slice ends inside a 64-wide stage (its last stage is zero-filled past the
 // edge).  Without it the main loop carries no edge logic.
 template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL>
@@ -169,6 +310,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     constexpr int NREAD = NREAD_RAW < TM * TN ? NREAD_RAW : TM * TN;
 
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    __shared__ __attribute__((aligned(256))) char pf_junk[256];
+    const uint32_t smem_lds = lds_addr(smem);   // LDS byte address of smem
+    const uint32_t junk_lds = lds_addr(pf_junk);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -188,6 +332,9 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     const int rows_a = g.M - m0, rows_b = g.N - n0;
     const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * 2);
     const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * 2);
+    // this lane's L2 prefetch line (full stages; the K-edge stage recomputes it)
+    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
+    const bool pf_on_a = wave == 0;
 
     // loop-invariant per-lane source offsets (full stages)
     uint32_t offa[TA::PER_WAVE], offb[TB::PER_WAVE];
@@ -215,21 +362,19 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
         const i32x4 ra = make_rsrc(Ab), rb = make_rsrc(Bb);
 
         auto load_stage = [&](int kt, int buf) {
-            char *base = smem + buf * STAGE;
+            const uint32_t base = smem_lds + buf * STAGE;
             if (!KTAIL || kt < nfull) {
 #pragma unroll
                 for (int i = 0; i < TA::PER_WAVE; ++i) {
                     const int seg = wave + i * NW;
                     if (TA::SEGS % NW == 0 || seg < TA::SEGS)
-                        raw_buffer_load_lds(ra, (MB_LDS uint32_t *)lds_ptr(base + seg * 1024), 16, (int)offa[i],
-                                            kt * stepa, 0, 0);
+                        dma16(ra, base + seg * 1024, offa[i], kt * stepa);
                 }
 #pragma unroll
                 for (int i = 0; i < TB::PER_WAVE; ++i) {
                     const int seg = wave + i * NW;
                     if (TB::SEGS % NW == 0 || seg < TB::SEGS)
-                        raw_buffer_load_lds(rb, (MB_LDS uint32_t *)lds_ptr(base + TA::BYTES + seg * 1024), 16,
-                                            (int)offb[i], kt * stepb, 0, 0);
+                        dma16(rb, base + TA::BYTES + seg * 1024, offb[i], kt * stepb);
                 }
             } else {
                 // the K edge: chunks past the slice end read as zeros
@@ -238,17 +383,21 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
                 for (int i = 0; i < TA::PER_WAVE; ++i) {
                     const int seg = wave + i * NW;
                     if (TA::SEGS % NW == 0 || seg < TA::SEGS)
-                        raw_buffer_load_lds(ra, (MB_LDS uint32_t *)lds_ptr(base + seg * 1024), 16,
-                                            (int)TA::src_offset(seg, lane, lda, rows_a, kleft), kt * stepa, 0, 0);
+                        dma16(ra, base + seg * 1024, TA::src_offset(seg, lane, lda, rows_a, kleft),
+                              kt * stepa);
                 }
 #pragma unroll
                 for (int i = 0; i < TB::PER_WAVE; ++i) {
                     const int seg = wave + i * NW;
                     if (TB::SEGS % NW == 0 || seg < TB::SEGS)
-                        raw_buffer_load_lds(rb, (MB_LDS uint32_t *)lds_ptr(base + TA::BYTES + seg * 1024), 16,
-                                            (int)TB::src_offset(seg, lane, ldb, rows_b, kleft), kt * stepb, 0, 0);
+                        dma16(rb, base + TA::BYTES + seg * 1024, TB::src_offset(seg, lane, ldb, rows_b, kleft),
+                              kt * stepb);
                 }
             }
+            const int kp = kt + kPfDist;
+            const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
+                              : pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+            pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
         };
 
         f32x16 acc[TN][TM];
@@ -275,6 +424,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 
         if (nk > 0) {
             load_stage(0, 0);
+            vm_wait_but_one();
             __syncthreads();
             read_frags(smem, 0, 0);
             if (nk > 1) load_stage(1, 1);
@@ -296,6 +446,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (kt + 1 < nk) {
+                vm_wait_but_one();   // this wave's loads of stage kt+1 have landed
                 __syncthreads();   // stage kt+1 landed everywhere; stage kt fully read
                 __builtin_amdgcn_sched_barrier(0);
                 read_frags(smem + ((kt + 1) & 1) * STAGE, 0, 0);
@@ -304,80 +455,184 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
             mma_step(1);
         }
 
-        // ---- epilogue: lane holds C[m][n_blk + 8*(r/4) + 4*(lane/32) + r%4] ----
-        const int mrow = lane & 31;
-        const int nsub = 4 * (lane >> 5);
-        T *Cb = (T *)g.c + bz * g.c_bs;
-        if (g.splits > 1) {
-            float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
-            const bool vec = (g.N & 3) == 0;
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    const int gm = m0 + wm * WTM + j * 32 + mrow;
-                    if (gm >= g.M) continue;
-                    float *row = ws + (int64_t)gm * g.N;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
-                        if (vec && gn + 3 < g.N) {
-                            *(float4 *)(row + gn) = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1],
-                                                                acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-                        } else {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (gn + r < g.N) row[gn + r] = acc[i][j][4 * q + r];
-                        }
-                    }
-                }
-        } else if (g.vec_ok && !g.epilogue) {
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    const int gm = m0 + wm * WTM + j * 32 + mrow;
-                    if (gm >= g.M) continue;
-                    T *row = Cb + gm * g.c_rs;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
-                        if (gn + 3 < g.N) {
-                            T o[4];
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
-                            uint2 u;
-                            __builtin_memcpy(&u, o, 8);
-                            *(uint2 *)(row + gn) = u;
-                        } else {
-#pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (gn + r < g.N) row[gn + r] = (T)acc[i][j][4 * q + r];
-                        }
-                    }
-                }
-        } else {
-#pragma unroll
-            for (int i = 0; i < TN; ++i)
-#pragma unroll
-                for (int j = 0; j < TM; ++j) {
-                    const int gm = m0 + wm * WTM + j * 32 + mrow;
-                    if (gm >= g.M) continue;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int gn = n0 + wn * WTN + i * 32 + 8 * q + nsub;
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int n = gn + r;
-                            if (n < g.N)
-                                store_out<T>(g, Cb + gm * g.c_rs + n * g.c_cs, acc[i][j][4 * q + r],
-                                             bz * g.bias_bs + gm * g.bias_rs + n * g.bias_cs);
-                        }
-                    }
-                }
-        }
+        store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         __syncthreads();   // LDS reuse by the next batch iteration
     }
+}
+
+// Ping-pong schedule of the 256 x 256 tile with 8 waves, two per SIMD (waves w and w + 4
+// share SIMD w % 4).  The waves form two groups, 0..3 and 4..7, that alternate between a
+// memory phase (all LDS fragment reads of one 64-deep stage into registers, plus this wave's
+// share of the LDS-direct prefetch) and a compute phase (the stage's 32 MFMAs back to back,
+// every operand already in registers).  Group 1 runs one phase behind group 0, so on each
+// SIMD one wave keeps the matrix core busy while the other feeds it; a workgroup barrier
+// separates the phases:
+//
+//   phase      2k                    2k+1                  2k+2
+//   group 0    read stage k,         compute stage k       read stage k+1,
+//              prefetch stage k+1                          prefetch stage k+2
+//   group 1    compute stage k-1,    read stage k          compute stage k,
+//              prefetch stage k+1                          prefetch stage k+2
+//
+// Stage k lives in buffer k % 2 during phases 2k and 2k+1; its buffer is refilled (stage
+// k+2) from phase 2k+2 on, after both groups read it.  Each wave waits for its own prefetch
+// at the end of odd phases, before the barrier that publishes the stage.
+template <class T, bool A_KC, bool B_KC, bool KTAIL>
+__global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
+    constexpr int BM = 256, BN = 256, WM = 2, NW = 8;
+    constexpr int WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
+    constexpr int BK = 64, KSTEPS = BK / 16;
+    using TA = Tile16<BM, NW, A_KC>;
+    using TB = Tile16<BN, NW, B_KC>;
+    constexpr int STAGE = TA::BYTES + TB::BYTES;
+
+    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    __shared__ __attribute__((aligned(256))) char pf_junk[256];
+    const uint32_t smem_lds = lds_addr(smem);
+    const uint32_t junk_lds = lds_addr(pf_junk);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int group = wave >> 2;
+    const int wm = wave % WM, wn = wave / WM;
+    const int tiles_m = cdiv(g.M, BM), tiles_n = cdiv(g.N, BN);
+    int tm, tn;
+    tile_coords16(blockIdx.x, tiles_m, tiles_n, g.swz, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.k_chunk;
+    const int kend = min(g.K, kbeg + g.k_chunk);
+    const int klen = kend - kbeg;
+    const int nk = cdiv(klen, BK);
+    const int nfull = klen / BK;
+    const int64_t lda = A_KC ? g.a_rs : g.a_cs;
+    const int64_t ldb = B_KC ? g.b_cs : g.b_rs;
+    const int rows_a = g.M - m0, rows_b = g.N - n0;
+    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * 2);
+    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * 2);
+    // this lane's L2 prefetch line (full stages; the K-edge stage recomputes it)
+    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
+    const bool pf_on_a = wave == 0;
+
+    uint32_t offa[TA::PER_WAVE], offb[TB::PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < TA::PER_WAVE; ++i) offa[i] = TA::src_offset(wave + i * NW, lane, lda, rows_a, BK);
+#pragma unroll
+    for (int i = 0; i < TB::PER_WAVE; ++i) offb[i] = TB::src_offset(wave + i * NW, lane, ldb, rows_b, BK);
+    int fba[A_KC ? 1 : TM], fbb[B_KC ? 1 : TN];
+#pragma unroll
+    for (int j = 0; j < (A_KC ? 1 : TM); ++j) fba[j] = TA::frag_base(wm * WTM, lane, j);
+#pragma unroll
+    for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
+
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
+        const T *Ab = (const T *)g.a + bz * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
+        const T *Bb = (const T *)g.b + bz * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
+        const i32x4 ra = make_rsrc(Ab), rb = make_rsrc(Bb);
+
+        // this wave's share (1/8) of stage kt into buffer kt % 2
+        auto prefetch = [&](int kt) {
+            const uint32_t base = smem_lds + (kt & 1) * STAGE;
+            if (!KTAIL || kt < nfull) {
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i) dma16(ra, base + (wave + i * NW) * 1024, offa[i], kt * stepa);
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i)
+                    dma16(rb, base + TA::BYTES + (wave + i * NW) * 1024, offb[i], kt * stepb);
+            } else {
+                const int kleft = klen - kt * BK;
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i)
+                    dma16(ra, base + (wave + i * NW) * 1024, TA::src_offset(wave + i * NW, lane, lda, rows_a, kleft),
+                          kt * stepa);
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i)
+                    dma16(rb, base + TA::BYTES + (wave + i * NW) * 1024,
+                          TB::src_offset(wave + i * NW, lane, ldb, rows_b, kleft), kt * stepb);
+            }
+            const int kp = kt + kPfDist;
+            const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
+                              : pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+            pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
+        };
+
+        f32x16 acc[TN][TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+        uint4 fa[KSTEPS][TM], fb[KSTEPS][TN];
+        auto read_stage = [&](int kt) {
+            const char *cur = smem + (kt & 1) * STAGE;
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s) {
+#pragma unroll
+                for (int j = 0; j < TM; ++j) fa[s][j] = TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+                    fb[s][i] = TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
+            }
+        };
+        auto compute_stage = [&]() {
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
+        };
+        auto phase_end = [&]() {
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+
+        if (nk > 0) {
+            prefetch(0);
+            vm_wait_but_one();
+            phase_end();
+            if (group == 0) {
+                for (int kt = 0; kt < nk; ++kt) {
+                    read_stage(kt);                 // phase 2kt
+                    if (kt + 1 < nk) prefetch(kt + 1);
+                    phase_end();
+                    compute_stage();                // phase 2kt+1
+                    vm_wait_but_one();
+                    phase_end();
+                }
+            } else {
+                if (nk > 1) prefetch(1);            // phase 0
+                phase_end();
+                for (int kt = 0; kt < nk; ++kt) {
+                    read_stage(kt);                 // phase 2kt+1
+                    vm_wait_but_one();
+                    phase_end();
+                    if (kt + 2 < nk) prefetch(kt + 2);   // phase 2kt+2
+                    compute_stage();
+                    if (kt + 1 < nk) phase_end();
+                }
+            }
+        }
+        store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        __syncthreads();   // LDS reuse by the next batch iteration
+    }
+}
+
+template <class T, bool KTAIL>
+hipError_t launch16pp(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    dim3 block(512);
+    if (a_kc && b_kc)
+        hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL>), grid, block, 0, st, g);
+    else if (a_kc && !b_kc)
+        hipLaunchKernelGGL((k_gemm16pp<T, true, false, KTAIL>), grid, block, 0, st, g);
+    else if (!a_kc && b_kc)
+        hipLaunchKernelGGL((k_gemm16pp<T, false, true, KTAIL>), grid, block, 0, st, g);
+    else
+        hipLaunchKernelGGL((k_gemm16pp<T, false, false, KTAIL>), grid, block, 0, st, g);
+    return hipGetLastError();
 }
 
 template <class T, int BM, int BN, int WM, int WN, bool KTAIL>

@@ -371,3 +371,20 @@ def test_gemv_config2_sizes(dev, n):
     assert_parity(mb.matmul(X8.to(dev), Wd), X8, W, tag="X8@W")
     Xn = torch.randn(n, 8, generator=g).to(torch.bfloat16)
     assert_parity(mb.matmul(Wd, Xn.to(dev)), W, Xn, tag="W@X8")
+
+
+# ---- every compiled 16-bit matrix-core schedule, forced, on edge shapes and all layouts ---------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("tile", [(256, 256, 64, 2, 4, 1), (256, 256, 64, 2, 4, 2), (256, 256, 64, 2, 2, 1),
+                                  (128, 128, 64, 2, 2, 1), (64, 64, 64, 2, 2, 1)], ids=str)
+@pytest.mark.parametrize("shape", [(256, 256, 64), (513, 257, 129), (1000, 700, 1000), (512, 768, 4160),
+                                   (64, 64, 4096)], ids=str)
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+def test_matrix_core_schedules(dev, dtype, tile, shape, layout):
+    M, N, K = shape
+    g = gen(hash((M, N, K, layout)) % 1000)
+    a = rand((M, K), dtype, g) if layout[0] == "r" else rand((K, M), dtype, g).t()
+    b = rand((K, N), dtype, g) if layout[1] == "r" else rand((N, K), dtype, g).t()
+    got = mb.matmul(_to(a, dev), _to(b, dev), backend="mpp", tile=tile)
+    assert_parity(got, a, b, tag=f"tile {tile} {dtype} {layout} {shape}")

@@ -214,7 +214,7 @@ def test_tile_candidates_primary_first():
     p = _lib.plan(d)
     cands = _lib.tile_candidates(d)
     assert len(cands) >= 2 and cands[0][:2] == tuple(p.tile[:2])
-    assert len(set(c[:5] for c in cands)) == len(cands)
+    assert len(set(c[:6] for c in cands)) == len(cands)
 
 
 # ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
