@@ -1,14 +1,22 @@
 """Benchmark of the metalblas matmul hot path on one MI355X.
 
-Headline (BASELINE.json metric): bf16 GEMM 8192^3 in TFLOP/s and % of the dense bf16 MFMA
-peak, plus bf16 GEMV 16384x16384 (y = W @ x) in GB/s and % of HBM peak.  One "step" is one
-8192^3 product C = A @ B (row-major A and B, synthetic N(0,1) inputs from a fixed seed,
-already resident in HBM).  Prints ONE JSON line.
+Headline (BASELINE.json ``metric``): bf16 GEMM 8192^3 in TFLOP/s and % of the dense bf16
+MFMA peak.  One "step" is one C = A @ B of row-major 8192 x 8192 bf16 operands (synthetic
+N(0,1) inputs from a fixed seed, resident in HBM before the timed region), i.e. one launch
+of the matrix-core GEMM kernel.  The other BASELINE configurations are measured the same
+way and reported under ``configs`` (GEMV 16384^2 in GB/s and % of HBM peak, the 2048 x 4096
+x 2048 layouts and addmm, fp16 bmm / broadcast / split-K, complex64 GEMM and GEMV, int8
+and int32 GEMM).  Prints ONE JSON line.
 
-Timing: HIP events on torch's current stream, which is the stream the library launches on.
-cpu_baseline: the CPU oracle (oracle/mb_oracle.c, a scalar port of the reference semantics)
-timed on a bounded sample of the same workload (a few output rows); cpu_torch: torch.matmul
-on the host cores for context (north star).
+Timing: HIP events (torch.cuda.Event) on torch's current stream, which is the stream the
+library launches its kernels on; W untimed warmup steps, then K timed steps bracketed by
+device synchronisation.  ``roofline.traffic`` is the HBM bytes per launch measured with
+rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a plain-copy calibration); the figures
+and the commands that produced them are in profiles/.
+
+cpu_baseline: the CPU oracle (oracle/mb_oracle.c, a scalar restatement of the reference's
+arithmetic) timed on whole output rows of the same 8192^3 workload for about --cpu-seconds;
+cpu_torch: torch.matmul on all host cores over a row slab of the same workload, for context.
 """
 from __future__ import annotations
 
@@ -21,8 +29,17 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-PEAK_BF16_TFLOPS = 2516.6     # 256 CU x 4096 flop/clk x 2.4 GHz (dense)
+# MI355X published dense peaks
+PEAK = {"bf16": 2516.6, "f16": 2516.6, "i8": 5033.2, "f32": 157.3}   # TFLOP/s (TOP/s for int8)
 PEAK_HBM_GBS = 8000.0
+
+# HBM bytes per launch from rocprofv3 --pmc (FETCH_SIZE x 2 + WRITE_SIZE x 1; the factors
+# come from a 1 GiB copy, which reads as 512 MiB of FETCH_SIZE and 1 GiB of WRITE_SIZE):
+# profiles/gemm_bf16_8192_pmc_traffic.md and profiles/gemv_bf16_16384_pmc_traffic.md
+TRAFFIC = {
+    "gemm_bf16_8192": 2.0621e9,
+    "gemv_bf16_16384": 5.3731e8,
+}
 
 
 def parse():
@@ -31,67 +48,193 @@ def parse():
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
     p.add_argument("--size", type=int, default=8192)
-    p.add_argument("--gemv", type=int, default=16384)
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
-    p.add_argument("--only", choices=["all", "gemm", "gemv", "copy"], default="all",
-                   help="copy: a plain 1 GiB device copy, the calibration run for HBM counters")
+    p.add_argument("--only", choices=["all", "gemm", "gemv", "configs", "copy"], default="all",
+                   help="gemm: the headline only; gemv: config 2 only; configs: every config but "
+                        "the headline; copy: a plain 1 GiB device copy (HBM counter calibration)")
     p.add_argument("--no-tune", action="store_true", help="static plans only (METALBLAS_AUTOTUNE=0)")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     return p.parse_args()
 
 
-def time_events(fn, steps):
-    import torch
+def time_events(torch, fn, steps, warmup):
+    """ms per call of fn over `steps` calls, after `warmup` untimed calls."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     s.record()
     for _ in range(steps):
         fn()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / steps   # ms per call
+    return s.elapsed_time(e) / steps
 
 
-def bench_gemm(mb, torch, n, steps, warmup):
-    g = torch.Generator().manual_seed(0)
+def _gen(torch, seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------------------------
+# headline: bf16 GEMM 8192^3
+# ---------------------------------------------------------------------------------------------
+
+def bench_headline(mb, torch, n, steps, warmup):
+    g = _gen(torch, 0)
     a_cpu = torch.randn(n, n, generator=g).to(torch.bfloat16)
     b_cpu = torch.randn(n, n, generator=g).to(torch.bfloat16)
     a, b = a_cpu.cuda(), b_cpu.cuda()
     out = torch.empty(n, n, dtype=torch.bfloat16, device="cuda")
-    for _ in range(warmup):
-        mb.matmul(a, b, out=out)
-    torch.cuda.synchronize()
-    ms = time_events(lambda: mb.matmul(a, b, out=out), steps)
+    mb.matmul(a, b, out=out)            # plan + autotune outside the timed region
+    ms = time_events(torch, lambda: mb.matmul(a, b, out=out), steps, warmup)
     plan = mb.kernels.plan(a, b)
-    return ms, plan, (a_cpu, b_cpu, out)
+    return ms, plan, (a_cpu, b_cpu)
 
 
-def bench_gemv(mb, torch, n, steps, warmup):
-    g = torch.Generator().manual_seed(1)
-    W_cpu = torch.randn(n, n, generator=g).to(torch.bfloat16)
-    x_cpu = torch.randn(n, generator=g).to(torch.bfloat16)
-    W, x = W_cpu.cuda(), x_cpu.cuda()
+# ---------------------------------------------------------------------------------------------
+# the other BASELINE configurations
+# ---------------------------------------------------------------------------------------------
+
+def _gemm_entry(name, ms, flops, peak_key, extra=None):
+    tf = flops / (ms * 1e-3) / 1e12
+    d = {"ms": round(ms, 5), "value": round(tf, 2), "unit": "TOP/s" if peak_key == "i8" else "TFLOP/s",
+         "roofline": {"bound": "mfma", "peak": PEAK[peak_key], "frac": round(tf / PEAK[peak_key], 4)}}
+    if extra:
+        d.update(extra)
+    return name, d
+
+
+def _gemv_entry(name, ms, nbytes, extra=None):
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    d = {"ms": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+         "roofline": {"bound": "hbm", "peak": PEAK_HBM_GBS, "frac": round(gbs / PEAK_HBM_GBS, 4),
+                      "algorithmic_bytes": int(nbytes)}}
+    if extra:
+        d.update(extra)
+    return name, d
+
+
+def bench_gemv(mb, torch, steps, warmup, n=16384):
+    """Config 2: bf16 W 16384 x 16384 row-major; W@x (row streams), x@W (column streams),
+    X(8 x K)@W (8 rows of x), W@X(K x 8)."""
+    g = _gen(torch, 1)
+    W = torch.randn(n, n, generator=g).to(torch.bfloat16).cuda()
+    x = torch.randn(n, generator=g).to(torch.bfloat16).cuda()
+    X8 = torch.randn(8, n, generator=g).to(torch.bfloat16).cuda()
+    Xn = torch.randn(n, 8, generator=g).to(torch.bfloat16).cuda()
+    res = {}
     y = torch.empty(n, dtype=torch.bfloat16, device="cuda")
-    for _ in range(warmup):
-        mb.matmul(W, x, out=y)
-    ms = time_events(lambda: mb.matmul(W, x, out=y), steps)
-    # x @ W (the column-streaming family) moves the same bytes
-    yt = torch.empty(n, dtype=torch.bfloat16, device="cuda")
-    for _ in range(warmup):
-        mb.matmul(x, W, out=yt)
-    ms_t = time_events(lambda: mb.matmul(x, W, out=yt), steps)
-    plan = mb.kernels.plan(W, x.reshape(-1, 1))
-    return ms, ms_t, plan, (W_cpu, x_cpu, y)
+    ms = time_events(torch, lambda: mb.matmul(W, x, out=y), steps, warmup)
+    res.update([_gemv_entry("gemv_W@x", ms, 2.0 * (n * n + 2 * n), {"plan": mb.kernels.plan(W, x[:, None])["family"]})])
+    ms = time_events(torch, lambda: mb.matmul(x, W, out=y), steps, warmup)
+    res.update([_gemv_entry("gemv_x@W", ms, 2.0 * (n * n + 2 * n), {"plan": mb.kernels.plan(x[None], W)["family"]})])
+    Y8 = torch.empty(8, n, dtype=torch.bfloat16, device="cuda")
+    ms = time_events(torch, lambda: mb.matmul(X8, W, out=Y8), steps, warmup)
+    res.update([_gemv_entry("gemv_X8@W", ms, 2.0 * (n * n + 16 * n))])
+    Yn = torch.empty(n, 8, dtype=torch.bfloat16, device="cuda")
+    ms = time_events(torch, lambda: mb.matmul(W, Xn, out=Yn), steps, warmup)
+    res.update([_gemv_entry("gemv_W@X8", ms, 2.0 * (n * n + 16 * n))])
+    return res
 
+
+def bench_layouts(mb, torch, steps, warmup, M=2048, K=4096, N=2048):
+    """Config 3: bf16 2048 x 4096 @ 4096 x 2048 in every operand layout, plus addmm."""
+    g = _gen(torch, 3)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = torch.randn(K, N, generator=g).to(torch.bfloat16)
+    dev = "cuda"
+    views = {
+        "rm_rm": (A.cuda(), B.cuda()),
+        "rm_cm": (A.cuda(), B.t().contiguous().cuda().t()),
+        "cm_rm": (A.t().contiguous().cuda().t(), B.cuda()),
+        "cm_cm": (A.t().contiguous().cuda().t(), B.t().contiguous().cuda().t()),
+        "row_sliced": (torch.randn(2 * M, K, generator=g).to(torch.bfloat16).cuda()[::2], B.cuda()),
+        "col_sliced": (torch.randn(M, 2 * K, generator=g).to(torch.bfloat16).cuda()[:, ::2], B.cuda()),
+        "offset17": (torch.cat([torch.zeros(17, dtype=torch.bfloat16), A.reshape(-1)]).cuda()[17:].view(M, K),
+                     B.cuda()),
+    }
+    flops = 2.0 * M * N * K
+    res = {}
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    for name, (a, b) in views.items():
+        ms = time_events(torch, lambda: mb.matmul(a, b, out=out), steps, warmup)
+        res.update([_gemm_entry(f"bf16_2048x4096x2048_{name}", ms, flops, "bf16",
+                                {"plan": mb.kernels.plan(a if name != "col_sliced" else a.contiguous(), b)["family"]})])
+    bias = torch.randn(N, generator=g).to(torch.bfloat16).cuda()
+    a, b = views["rm_rm"]
+    ms = time_events(torch, lambda: mb.addmm(bias, a, b, beta=0.5, alpha=2.0, out=out), steps, warmup)
+    res.update([_gemm_entry("bf16_2048x4096x2048_addmm", ms, flops, "bf16")])
+    return res
+
+
+def bench_bmm(mb, torch, steps, warmup):
+    """Config 4: fp16 bmm 8 x (512x256 @ 256x512), broadcast B, split-K 1 x 128 x 65536."""
+    g = _gen(torch, 4)
+    a = torch.randn(8, 512, 256, generator=g).to(torch.float16).cuda()
+    b = torch.randn(8, 256, 512, generator=g).to(torch.float16).cuda()
+    b2 = torch.randn(256, 512, generator=g).to(torch.float16).cuda()
+    res = {}
+    fl = 2.0 * 8 * 512 * 512 * 256
+    ms = time_events(torch, lambda: mb.bmm(a, b), steps, warmup)
+    res.update([_gemm_entry("f16_bmm_8x512x512x256", ms, fl, "f16")])
+    ms = time_events(torch, lambda: mb.matmul(a, b2), steps, warmup)
+    res.update([_gemm_entry("f16_bmm_broadcastB", ms, fl, "f16")])
+    ak = torch.randn(1, 128, 65536, generator=g).to(torch.float16).cuda()
+    bk = torch.randn(1, 65536, 128, generator=g).to(torch.float16).cuda()
+    ms = time_events(torch, lambda: mb.bmm(ak, bk), steps, warmup)
+    nbytes = 2.0 * (2 * 128 * 65536 + 128 * 128)
+    name, d = _gemm_entry("f16_splitk_128x128x65536", ms, 2.0 * 128 * 128 * 65536, "f16")
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    d["hbm"] = {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                "note": "arithmetic intensity 64 flop/B: HBM-bound"}
+    res[name] = d
+    return res
+
+
+def bench_mixed(mb, torch, steps, warmup):
+    """Config 5: complex64 GEMM 2048^3 with conj(A), complex64 GEMV 8192^2, int8 GEMM 4096^3;
+    config 1: int32 GEMM 256^3."""
+    g = _gen(torch, 5)
+    res = {}
+    n = 2048
+    a = torch.complex(torch.randn(n, n, generator=g), torch.randn(n, n, generator=g)).cuda()
+    b = torch.complex(torch.randn(n, n, generator=g), torch.randn(n, n, generator=g)).cuda()
+    ms = time_events(torch, lambda: mb.matmul(a.conj(), b), steps, warmup)
+    res.update([_gemm_entry("c64_gemm_2048_conjA", ms, 8.0 * n ** 3, "f32",
+                            {"plan": mb.kernels.plan(a, b)["family"]})])
+    m = 8192
+    A = torch.complex(torch.randn(m, m, generator=g), torch.randn(m, m, generator=g)).cuda()
+    x = torch.complex(torch.randn(m, generator=g), torch.randn(m, generator=g)).cuda()
+    ms = time_events(torch, lambda: mb.matmul(A, x), steps, warmup)
+    res.update([_gemv_entry("c64_gemv_8192", ms, 8.0 * (m * m + 2 * m))])
+    del A, x
+    k = 4096
+    ai = torch.randint(-4, 5, (k, k), generator=g, dtype=torch.int8).cuda()
+    bi = torch.randint(-4, 5, (k, k), generator=g, dtype=torch.int8).cuda()
+    ms = time_events(torch, lambda: mb.matmul(ai, bi), steps, warmup)
+    res.update([_gemm_entry("i8_gemm_4096", ms, 2.0 * k ** 3, "i8", {"plan": mb.kernels.plan(ai, bi)["family"]})])
+    s = 256
+    a32 = torch.randint(-8, 9, (s, s), generator=g, dtype=torch.int32).cuda()
+    b32 = torch.randint(-8, 9, (s, s), generator=g, dtype=torch.int32).cuda()
+    ms = time_events(torch, lambda: mb.matmul(a32, b32), steps, warmup)
+    res["i32_gemm_256"] = {"ms": round(ms, 5), "us": round(ms * 1e3, 2),
+                           "value": round(2.0 * s ** 3 / (ms * 1e-3) / 1e9, 1), "unit": "GOP/s",
+                           "roofline": {"bound": "launch", "note": "33.6 M int-ops: launch/latency bound"},
+                           "plan": mb.kernels.plan(a32, b32)["family"]}
+    return res
+
+
+# ---------------------------------------------------------------------------------------------
+# CPU baselines
+# ---------------------------------------------------------------------------------------------
 
 def cpu_oracle_gemm(a_cpu, b_cpu, seconds):
-    """Time the scalar oracle on whole output rows until ~seconds have elapsed."""
+    """The scalar oracle on whole output rows of the workload until ~seconds have elapsed."""
     import oracle
     n = a_cpu.shape[0]
-    rows_done = 0
+    rows_done, r = 0, 0
     t0 = time.perf_counter()
-    r = 0
     while True:
         oracle.gemm(a_cpu, b_cpu, rows=[r])
         rows_done += 1
@@ -104,12 +247,11 @@ def cpu_oracle_gemm(a_cpu, b_cpu, seconds):
 
 
 def cpu_torch_gemm(torch, a_cpu, b_cpu, seconds):
-    """torch.matmul on the host cores over a row slab of the same workload."""
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     rows = 256
     a = a_cpu[:rows]
-    torch.matmul(a, b_cpu)   # warmup
+    torch.matmul(a, b_cpu)
     t0 = time.perf_counter()
     it = 0
     while True:
@@ -125,81 +267,75 @@ def cpu_torch_gemm(torch, a_cpu, b_cpu, seconds):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only (--gpus 1); the multi-GPU "
-                          "sharding is a design in DESIGN.md, not a measured path"}))
+        print(json.dumps({"error": "this build measures one GPU: run with --gpus 1 (the multi-GPU "
+                          "sharding of the path is a design, not a measured configuration)"}))
         sys.exit(2)
     if args.no_tune:
         os.environ["METALBLAS_AUTOTUNE"] = "0"
     import torch
     import metalblas_amd as mb
+
     if args.only == "copy":
         nbytes = 1 << 30
         src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
         dst = torch.empty_like(src)
-        for _ in range(args.warmup):
-            dst.copy_(src)
-        ms = time_events(lambda: dst.copy_(src), args.steps)
+        ms = time_events(torch, lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"copy_bytes_each_way": nbytes, "ms": round(ms, 4),
                           "GBps_read_plus_write": round(2 * nbytes / ms / 1e6, 1)}))
         return
 
+    n = args.size
     result = {
         "metric": "TFLOP/s + % MFMA peak (bf16 GEMM 8192³); GEMV HBM GB/s + % peak",
-        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic N(0,1) bf16 inputs from torch.Generator seed 0, resident in HBM",
-        "config": {"workload": f"bf16 GEMM C=A@B {args.size}x{args.size}x{args.size}, row-major A and B "
-                               "(BASELINE config 3, square case)",
-                   "gemv_workload": f"bf16 GEMV y=W@x W {args.gemv}x{args.gemv} row-major (config 2)",
-                   "parallelism": "single GPU"},
+        "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) inputs from torch.Generator seeds, resident in HBM",
+        "config": {"workload": f"bf16 GEMM C = A @ B, {n} x {n} x {n}, row-major A and B "
+                               "(BASELINE config 3, square case)", "parallelism": "single GPU"},
     }
-    gemm_data = gemv_data = None
+    headline = None
     if args.only in ("all", "gemm"):
-        n = args.size
-        ms, plan, gemm_data = bench_gemm(mb, torch, n, args.steps, args.warmup)
-        flops = 2.0 * n * n * n
-        tflops = flops / (ms * 1e-3) / 1e12
-        result["value"] = round(tflops, 2)
+        ms, plan, headline = bench_headline(mb, torch, n, args.steps, args.warmup)
+        flops = 2.0 * n ** 3
+        tf = flops / (ms * 1e-3) / 1e12
+        result["value"] = round(tf, 2)
         result["ms_per_step"] = round(ms, 4)
         result["roofline"] = {
-            "bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "kernel": f"k_gemm_mfma<bf16,{plan['tile'][0]},{plan['tile'][1]}>",
+            "bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
+            "frac": round(tf / PEAK["bf16"], 4),
+            "traffic": TRAFFIC["gemm_bf16_8192"] if n == 8192 else None,
+            "kernel": f"matrix-core GEMM tile {plan['tile'][0]}x{plan['tile'][1]} "
+                      f"schedule {'ping-pong' if plan['tile'][5] == 2 else 'interleaved'}",
             "algorithmic_per_launch": f"2*{n}^3 = {flops:.4e} flop",
             "avg_launch_ms": round(ms, 4),
         }
         result["plan"] = {k: plan[k] for k in ("family", "tile", "split_k", "grid")}
-    if args.only in ("all", "gemv"):
-        n = args.gemv
-        ms, ms_t, plan, gemv_data = bench_gemv(mb, torch, n, args.steps, args.warmup)
-        nbytes = 2.0 * (n * n + n + n)
-        gbs = nbytes / (ms * 1e-3) / 1e9
-        gbs_t = nbytes / (ms_t * 1e-3) / 1e9
-        result["gemv"] = {
-            "value": round(gbs, 1), "unit": "GB/s", "ms": round(ms, 4),
-            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                         "algorithmic_per_launch": f"2*({n}^2+2*{n}) = {nbytes:.4e} B"},
-            "x_at_W": {"value": round(gbs_t, 1), "unit": "GB/s", "ms": round(ms_t, 4),
-                       "frac": round(gbs_t / PEAK_HBM_GBS, 4)},
-            "plan": plan["family"],
-        }
+    if args.only in ("all", "gemv", "configs"):
+        cfg = {}
+        cfg.update(bench_gemv(mb, torch, args.steps, args.warmup))
+        if args.only != "gemv":
+            cfg.update(bench_layouts(mb, torch, args.steps, args.warmup))
+            cfg.update(bench_bmm(mb, torch, args.steps, args.warmup))
+            cfg.update(bench_mixed(mb, torch, args.steps, args.warmup))
+        g = cfg["gemv_W@x"]
+        g["roofline"]["traffic"] = TRAFFIC["gemv_bf16_16384"]
+        result["configs"] = cfg
         if result["value"] is None:
-            result.update({"value": round(gbs, 1), "unit": "GB/s", "ms_per_step": round(ms, 4)})
-    if not args.no_cpu and gemm_data is not None:
-        a_cpu, b_cpu, _ = gemm_data
+            result.update({"value": g["value"], "unit": "GB/s", "ms_per_step": g["ms"],
+                           "roofline": dict(g["roofline"], achieved=g["value"], unit="GB/s")})
+    if not args.no_cpu and headline is not None:
+        a_cpu, b_cpu = headline
         v, rows, el = cpu_oracle_gemm(a_cpu, b_cpu, args.cpu_seconds)
         result["cpu_baseline"] = {
             "value": round(v, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"oracle/mb_oracle.c (scalar fp64 restatement) on {rows} output rows of the "
-                      f"{args.size}^3 bf16 GEMM, {el:.1f} s",
+            "sample": f"oracle/mb_oracle.c (scalar fp64 restatement) on {rows} whole output rows of the "
+                      f"{n}^3 bf16 GEMM, {el:.1f} s",
         }
         v2, rows2, it2, thr = cpu_torch_gemm(torch, a_cpu, b_cpu, max(2.0, args.cpu_seconds / 2))
-        result["cpu_torch"] = {
-            "value": round(v2, 4), "unit": "TFLOP/s", "cores": thr, "kind": "torch.matmul bf16 CPU",
-            "sample": f"{rows2}x{args.size}x{args.size} slab x{it2}",
-        }
+        result["cpu_torch"] = {"value": round(v2, 4), "unit": "TFLOP/s", "cores": thr,
+                               "kind": "torch.matmul bf16 on the host CPU",
+                               "sample": f"{rows2} x {n} x {n} slab x {it2}"}
     print(json.dumps(result))
 
 

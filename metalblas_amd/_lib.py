@@ -153,7 +153,7 @@ def make_desc(dtype, batch, M, N, K, a, b, c, bias=None, *, conj_a=False, conj_b
     """Build a descriptor.  a/b/c/bias are (tensor, row_stride, col_stride, batch_stride).
 
     epilogue: None or (beta, alpha, beta_nz, alpha_nz) with beta/alpha already cast the way
-    metalblas/dispatch.py:146-150 (_scalars) casts them.
+    metalblas/dispatch.py:127-131 (_scalars) casts them.
     """
     d = MbGemmDesc()
     d.dtype = DTYPE_CODE[dtype]

@@ -5,15 +5,15 @@ metalblas/dispatch.py (Isalia20/metalBLAS); only the device changes from ``mps``
 PyTorch-ROCm tensor (``device.type == "cuda"``).  The arithmetic runs in the hand-written
 HIP kernels of libmetalblas_hip.so, reached through the C ABI (``_lib``).
 
-Routing follows metalblas/dispatch.py:193-204: complex if either operand is complex,
+Routing follows metalblas/dispatch.py:174-185: complex if either operand is complex,
 integer if ``a`` is an integer tensor, floating point otherwise.  Differences from the
 reference that change no result:
   * conjugated operands are passed as a conj flag instead of being materialised
     (metalblas/complex_dispatch.py:25-30 resolves them by copying);
   * batched integer/complex products run as one batched kernel instead of a Python loop
-    (metalblas/dispatch.py:153-164, integer_dispatch.py:125-127);
+    (metalblas/dispatch.py:134-145, integer_dispatch.py:125-127);
   * outputs are freshly allocated (the reference's pooled outputs can alias a returned view,
-    metalblas/dispatch.py:92-112 with :186-189);
+    metalblas/dispatch.py:78-93 with :167-170);
   * ``out=`` tensors of any stride are written in place.
 """
 from __future__ import annotations
@@ -51,7 +51,7 @@ def _on_device(t) -> bool:
 
 def _unit_lead(t, rows, cols):
     """``(is_column_major, leading_stride)`` for a simple matrix view, else None
-    (metalblas/dispatch.py:42-49)."""
+    (metalblas/dispatch.py:23-30)."""
     s0, s1 = map(int, t.stride()[-2:])
     if s1 == 1 and s0 >= cols:
         return False, s0
@@ -61,7 +61,7 @@ def _unit_lead(t, rows, cols):
 
 
 def _matrix_view(t, rows, cols):
-    """Keep row/column-major views, copy anything else (metalblas/dispatch.py:52-54)."""
+    """Keep row/column-major views, copy anything else (metalblas/dispatch.py:33-35)."""
     return t if _unit_lead(t, rows, cols) else t.contiguous()
 
 
@@ -73,7 +73,7 @@ def _mat(t):
 
 
 def _scalars(dtype, beta, alpha):
-    """Cast beta/alpha like metalblas/dispatch.py:146-150 and report which terms are live."""
+    """Cast beta/alpha like metalblas/dispatch.py:127-131 and report which terms are live."""
     if dtype in INT_DTYPES:
         beta, alpha = int(beta), int(alpha)
     elif dtype not in COMPLEX_DTYPES:
@@ -202,12 +202,12 @@ def _complex_matmul(a, b, out=None, epilogue=None):
 
 
 # ---------------------------------------------------------------------------------------
-# Public API (metalblas/dispatch.py:167-321)
+# Public API (metalblas/dispatch.py:148-302)
 # ---------------------------------------------------------------------------------------
 
 def _matmul_nd(a, b, out=None):
     """Vector promotion and broadcast batches around the 2-D/3-D kernels
-    (metalblas/dispatch.py:167-190)."""
+    (metalblas/dispatch.py:148-171)."""
     assert a.ndim and b.ndim, "matmul operands must be at least 1-D"
     a_vec, b_vec = a.ndim == 1, b.ndim == 1
     if a_vec:
@@ -235,7 +235,7 @@ def _matmul_nd(a, b, out=None):
 def matmul(a: torch.Tensor, b: torch.Tensor, *, backend: str | None = None,
            tile: tuple | None = None, swizzle_log: int | None = None,
            out: torch.Tensor | None = None) -> torch.Tensor:
-    """Compute ``a @ b`` on the GPU (metalblas/dispatch.py:193-204)."""
+    """Compute ``a @ b`` on the GPU (metalblas/dispatch.py:174-185)."""
     if a.ndim != 2 or b.ndim != 2:
         return _matmul_nd(a, b, out)
     if _on_device(a) and (a.dtype in COMPLEX_DTYPES or b.dtype in COMPLEX_DTYPES):
@@ -248,7 +248,7 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, backend: str | None = None,
 def addmm(input: torch.Tensor, mat1: torch.Tensor, mat2: torch.Tensor, *,
           beta=1, alpha=1, out: torch.Tensor | None = None) -> torch.Tensor:
     """Compute ``beta * input + alpha * (mat1 @ mat2)`` with one final rounding
-    (metalblas/dispatch.py:207-227)."""
+    (metalblas/dispatch.py:188-208)."""
     assert _on_device(mat1) and _on_device(mat2)
     assert mat1.dim() == 2 and mat2.dim() == 2, "addmm expects 2-D mat1, mat2"
     M, K = mat1.shape
@@ -271,7 +271,7 @@ def addmm(input: torch.Tensor, mat1: torch.Tensor, mat2: torch.Tensor, *,
 
 
 def _bmm_shape(a, b, op):
-    """metalblas/dispatch.py:136-143."""
+    """metalblas/dispatch.py:117-124."""
     assert _on_device(a) and _on_device(b), f"{op} expects cuda tensors"
     assert a.dim() == 3 and b.dim() == 3, f"{op} expects 3-D inputs"
     assert a.dtype == b.dtype, f"{op} requires both operands the same dtype"
@@ -302,7 +302,7 @@ def _batched(a, b, out, Bb, M, N, K, dtype, bias=None, epilogue=None):
 
 def bmm(a: torch.Tensor, b: torch.Tensor, *,
         out: torch.Tensor | None = None) -> torch.Tensor:
-    """Batched 3-D matrix multiplication (metalblas/dispatch.py:230-244)."""
+    """Batched 3-D matrix multiplication (metalblas/dispatch.py:211-225)."""
     Bb, M, N, K, dtype = _bmm_shape(a, b, "bmm")
     if Bb == 0 or M == 0 or N == 0:
         return out if out is not None else a.new_empty(Bb, M, N)
@@ -314,7 +314,7 @@ def bmm(a: torch.Tensor, b: torch.Tensor, *,
 
 def baddbmm(input: torch.Tensor, batch1: torch.Tensor, batch2: torch.Tensor, *,
             beta=1, alpha=1, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``beta * input + alpha * (batch1 @ batch2)`` (metalblas/dispatch.py:247-261)."""
+    """``beta * input + alpha * (batch1 @ batch2)`` (metalblas/dispatch.py:228-242)."""
     Bb, M, N, K, dtype = _bmm_shape(batch1, batch2, "baddbmm")
     beta, alpha, bnz, anz = _scalars(dtype, beta, alpha)
     o = _bmm_out(batch1, out, Bb, M, N, dtype)
@@ -330,7 +330,7 @@ def baddbmm(input: torch.Tensor, batch1: torch.Tensor, batch2: torch.Tensor, *,
 def addbmm(input: torch.Tensor, batch1: torch.Tensor, batch2: torch.Tensor, *,
            beta=1, alpha=1, out: torch.Tensor | None = None) -> torch.Tensor:
     """``beta * input + alpha * sum_b(batch1[b] @ batch2[b])`` as one addmm with K' = Bb*K
-    (metalblas/dispatch.py:264-279)."""
+    (metalblas/dispatch.py:245-260)."""
     Bb, M, N, K, dtype = _bmm_shape(batch1, batch2, "addbmm")
     if Bb == 0 or K == 0:
         # beta * input broadcast to (M, N): a K == 0 product with the fused epilogue
@@ -343,7 +343,7 @@ def addbmm(input: torch.Tensor, batch1: torch.Tensor, batch2: torch.Tensor, *,
 
 
 def dot(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """1-D inner product, matching ``torch.dot`` (metalblas/dispatch.py:282-290)."""
+    """1-D inner product, matching ``torch.dot`` (metalblas/dispatch.py:263-271)."""
     assert a.dim() == 1 and b.dim() == 1, \
         f"1D tensors expected, but got {a.dim()}D and {b.dim()}D tensors"
     assert a.shape[0] == b.shape[0], \
@@ -354,12 +354,12 @@ def dot(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def vdot(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """Inner product conjugating the first argument (metalblas/dispatch.py:293-295)."""
+    """Inner product conjugating the first argument (metalblas/dispatch.py:274-276)."""
     return dot(a.conj() if a.is_complex() else a, b)
 
 
 def outer(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
-    """Outer product of two vectors (metalblas/dispatch.py:298-302), computed as the K == 1
+    """Outer product of two vectors (metalblas/dispatch.py:279-283), computed as the K == 1
     product ``a[:, None] @ b[None, :]``; mixed dtypes promote as torch's ``*`` does."""
     assert a.dim() == 1, f"outer: Expected 1-D argument self, but got {a.dim()}-D"
     assert b.dim() == 1, f"outer: Expected 1-D argument vec2, but got {b.dim()}-D"
@@ -370,7 +370,7 @@ def outer(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
 
 
 def mv(mat: torch.Tensor, vec: torch.Tensor) -> torch.Tensor:
-    """Matrix-vector product (metalblas/dispatch.py:305-311)."""
+    """Matrix-vector product (metalblas/dispatch.py:286-292)."""
     assert mat.dim() == 2 and vec.dim() == 1, \
         f"vector + matrix @ vector expected, got {mat.dim()}, {mat.dim()}, {vec.dim()}"
     assert mat.shape[1] == vec.shape[0], \

@@ -99,7 +99,7 @@ def gemm(a, b, *, bias=None, beta=None, alpha=None, rows=None):
     """Oracle product of CPU tensors a (M x K or B x M x K) and b (K x N or B x K x N).
 
     bias: tensor broadcastable to the output (expanded here); beta/alpha: the epilogue
-    scalars (already cast as metalblas/dispatch.py:146-150 casts them), both None = plain
+    scalars (already cast as metalblas/dispatch.py:127-131 casts them), both None = plain
     product.  rows: optional list of output rows to compute (2-D only).
     Returns (c, exact).
     """

@@ -129,7 +129,7 @@ def check_fused(dev, op, shape, dtype, bshape, beta=1, alpha=1, seed=0):
     bias = rand(bshape, dtype, g)
     got = getattr(mb, op)(bias.to(dev), a.to(dev), b.to(dev), beta=beta, alpha=alpha)
     tag = f"{op} {dtype} {shape} bias={bshape} beta={beta} alpha={alpha}"
-    # scalars as metalblas/dispatch.py:146-150 casts them
+    # scalars as metalblas/dispatch.py:127-131 casts them
     if dtype in INTS:
         cb, ca = int(beta), int(alpha)
     elif dtype in COMPLEX:
@@ -301,7 +301,7 @@ def test_vectors(dev, dtype):
 
 
 def test_empty_and_k0(dev):
-    """metalblas/dispatch.py:234-237: empty batch -> empty, K == 0 -> zeros."""
+    """metalblas/dispatch.py:215-218: empty batch -> empty, K == 0 -> zeros."""
     a = torch.randn(3, 4, 0, device=dev)
     b = torch.randn(3, 0, 5, device=dev)
     r = mb.bmm(a, b)
