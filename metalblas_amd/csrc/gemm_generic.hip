@@ -151,12 +151,53 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
     }
 }
 
+// Operand copy (PackArgs): each thread writes 4 consecutive elements along the destination's
+// contiguous dimension (coalesced stores); source reads follow the source strides.  The grid
+// is x: inner chunks, y: outer index (grid-stride), z: batch (grid-stride).
+template <class E>
+__global__ __launch_bounds__(256) void k_pack(PackArgs a) {
+    const int64_t inner_n = a.contig_cols ? a.cols_p : a.rows_p;
+    const int64_t outer_n = a.contig_cols ? a.rows_p : a.cols_p;
+    const int64_t i0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i0 >= inner_n) return;
+    for (int64_t bz = blockIdx.z; bz < a.batch; bz += gridDim.z) {
+        const E *src = (const E *)a.src + bz * a.s_bs;
+        E *dst = (E *)a.dst + bz * a.d_bs;
+        for (int64_t o = blockIdx.y; o < outer_n; o += gridDim.y) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t i = i0 + j;
+                if (i >= inner_n) break;
+                const int64_t r = a.contig_cols ? o : i, c = a.contig_cols ? i : o;
+                E v = E(0);
+                if (r < a.rows && c < a.cols) v = src[r * a.s_rs + c * a.s_cs];
+                dst[r * a.d_rs + c * a.d_cs] = v;
+            }
+        }
+    }
+}
+
 inline int elementwise_blocks(int64_t total) {
     int64_t b = (total + 255) / 256;
     return (int)(b < 65536 ? (b < 1 ? 1 : b) : 65536);
 }
 
 }  // namespace
+
+hipError_t launch_pack(const PackArgs &a, hipStream_t st) {
+    const int64_t inner_n = a.contig_cols ? a.cols_p : a.rows_p;
+    const int64_t outer_n = a.contig_cols ? a.rows_p : a.cols_p;
+    dim3 grid((unsigned)((inner_n + 1023) / 1024), (unsigned)(outer_n < 65535 ? outer_n : 65535),
+              (unsigned)(a.batch < 65535 ? a.batch : 65535));
+    switch (a.es) {
+        case 1: hipLaunchKernelGGL(k_pack<uint8_t>, grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(k_pack<uint16_t>, grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_pack<uint32_t>, grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(k_pack<uint64_t>, grid, dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape) {
     const int tiles = cdiv(g.M, GBM) * cdiv(g.N, GBN);

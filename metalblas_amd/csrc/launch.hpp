@@ -78,7 +78,20 @@ struct LaunchShape {
     dim3 grid, block;
 };
 
+// Operand copy into a loader-friendly layout: dst(b, r, c) = src(b, r, c) for r < rows,
+// c < cols, and 0 in the padding up to rows_p x cols_p.  Strides are in elements.
+struct PackArgs {
+    const void *src;
+    void *dst;
+    int64_t s_rs, s_cs, s_bs;
+    int64_t d_rs, d_cs, d_bs;
+    int32_t rows, cols, rows_p, cols_p, batch;
+    int32_t contig_cols;   // 1: destination contiguous along columns (d_cs == 1), else rows
+    int32_t es;            // element bytes: 1, 2, 4 or 8
+};
+
 // gemm_generic.hip
+hipError_t launch_pack(const PackArgs &a, hipStream_t st);
 hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st);

@@ -39,11 +39,23 @@ struct Prob {
     int swz;
     int split_req;
     bool transposed;
+    bool a_padded = false, b_padded = false;   // workspace copies, contiguous extent zero-padded
+};
+
+// A strided operand copied into the workspace in a layout the matrix-core loaders can stream
+// (16-byte aligned base and leading dimension, the contiguous extent padded to a 16-byte
+// multiple with zeros).
+struct PackOp {
+    bool on = false;
+    int64_t off = 0;        // byte offset of the copy in the workspace
+    PackArgs a;             // source / destination strides and extents (dst pointer set at run)
 };
 
 struct Plan {
     int family = MB_FAMILY_NONE;
     Prob p;
+    PackOp pack[2];           // A, B
+    int64_t split_off = 0;    // workspace byte offset of the split-K partial planes
     // GEMV
     GemvArgs gv;
     bool gemv_dot = false;
@@ -299,34 +311,76 @@ MfmaTile snap_tile(int dt, const int32_t *t) {
     return list[best];
 }
 
+// Orientation of an operand: 1 = contiguous along K, 0 = contiguous along M (A) / N (B),
+// -1 = no unit stride.
+int a_orient(const Prob &p) { return p.a.cs == 1 ? 1 : p.a.rs == 1 ? 0 : -1; }
+int b_orient(const Prob &p) { return p.b.rs == 1 ? 1 : p.b.cs == 1 ? 0 : -1; }
+
+// Can the matrix-core loaders stream this operand in place?  16-byte aligned base, leading
+// dimension and batch stride, and the contiguous extent a multiple of 16 bytes (chunks never
+// straddle the end of a row).
+bool operand_ok(const Operand &o, int orient, bool is_a, const Prob &p) {
+    const int es = dtype_size(p.dt), E = 16 / es;
+    if (orient < 0) return false;
+    const bool kc = orient == 1;
+    const int64_t ld = is_a ? (kc ? o.rs : o.cs) : (kc ? o.cs : o.rs);
+    const int64_t contig = kc ? p.K : (is_a ? p.M : p.N);
+    const bool padded = is_a ? p.a_padded : p.b_padded;   // the chunk past the end reads zeros
+    if ((ld * es) % 16 || (!padded && contig % E)) return false;
+    if (!aligned(o.ptr, 16) || (p.batch > 1 && (o.bs * es) % 16)) return false;
+    return true;
+}
+
 bool mfma_layout_ok(const Prob &p, bool &a_kc, bool &b_kc) {
     if (!mfma_supported_dtype(p.dt)) return false;
-    const int es = dtype_size(p.dt);
-    const int E = 16 / es;
-    const bool batched = p.batch > 1;
-    // A
-    if (p.a.cs == 1) {
-        a_kc = true;
-        if ((p.a.rs * es) % 16 || p.K % E) return false;
-    } else if (p.a.rs == 1) {
-        a_kc = false;
-        if ((p.a.cs * es) % 16 || p.M % E) return false;
-    } else {
-        return false;
+    const int oa = a_orient(p), ob = b_orient(p);
+    a_kc = oa == 1;
+    b_kc = ob == 1;
+    return operand_ok(p.a, oa, true, p) && operand_ok(p.b, ob, false, p);
+}
+
+// Plan workspace copies of the operands the loaders cannot stream in place (the reference's
+// storage-offset views such as a 17-element offset, odd leading dimensions, K not a multiple
+// of 16 bytes).  The copy keeps the operand's orientation (K-contiguous if it has no unit
+// stride) and zero-pads the contiguous extent; when K is padded every K-contiguous operand
+// is copied so that the padding contributes zeros.  Returns the workspace bytes used.
+int64_t plan_packs(Prob &p, Plan &pl) {
+    const int es = dtype_size(p.dt), E = 16 / es;
+    int64_t ws = 0;
+    const char *placeholder = (const char *)(uintptr_t)4096;   // aligned stand-in until run time
+    for (int which = 0; which < 2; ++which) {
+        const bool is_a = which == 0;
+        Operand &o = is_a ? p.a : p.b;
+        int orient = is_a ? a_orient(p) : b_orient(p);
+        bool need = !operand_ok(o, orient, is_a, p);
+        if (orient < 0) orient = 1;
+        if (orient == 1 && p.K % E) need = true;
+        if (!need) continue;
+        PackOp &pk = pl.pack[which];
+        PackArgs &a = pk.a;
+        memset(&a, 0, sizeof(a));
+        // logical matrix: A is M x K, B is K x N
+        a.rows = (int)(is_a ? p.M : p.K);
+        a.cols = (int)(is_a ? p.K : p.N);
+        a.contig_cols = is_a ? (orient == 1) : (orient == 0);
+        const int64_t rows_p = a.contig_cols ? a.rows : (a.rows + E - 1) / E * E;
+        const int64_t cols_p = a.contig_cols ? (a.cols + E - 1) / E * E : a.cols;
+        a.rows_p = (int)rows_p;
+        a.cols_p = (int)cols_p;
+        a.batch = o.bs == 0 ? 1 : (int)p.batch;
+        a.src = o.ptr;
+        a.s_rs = o.rs; a.s_cs = o.cs; a.s_bs = o.bs;
+        a.d_rs = a.contig_cols ? cols_p : 1;
+        a.d_cs = a.contig_cols ? 1 : rows_p;
+        a.d_bs = o.bs == 0 ? 0 : rows_p * cols_p;
+        a.es = es;
+        pk.on = true;
+        pk.off = ws;
+        ws += (rows_p * cols_p * a.batch * es + 255) / 256 * 256;
+        o = {placeholder, a.d_rs, a.d_cs, a.d_bs};
+        (is_a ? p.a_padded : p.b_padded) = true;
     }
-    if (!aligned(p.a.ptr, 16) || (batched && (p.a.bs * es) % 16)) return false;
-    // B
-    if (p.b.rs == 1) {
-        b_kc = true;
-        if ((p.b.cs * es) % 16 || p.K % E) return false;
-    } else if (p.b.cs == 1) {
-        b_kc = false;
-        if ((p.b.rs * es) % 16 || p.N % E) return false;
-    } else {
-        return false;
-    }
-    if (!aligned(p.b.ptr, 16) || (batched && (p.b.bs * es) % 16)) return false;
-    return true;
+    return ws;
 }
 
 void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
@@ -445,7 +499,21 @@ void plan_generic(const Prob &p, Plan &pl) {
     pl.family = MB_FAMILY_GENERIC;
 }
 
-int make_plan(const mb_gemm_desc *d, Plan &pl) {
+// A plan that uses no workspace: one K slice.
+void drop_splits(Plan &pl) {
+    pl.ws_bytes = 0;
+    pl.split_off = 0;
+    if (pl.family == MB_FAMILY_GEMV_AXPY) {
+        pl.gv.splits = 1;
+        pl.gv.k_chunk = pl.gv.K;
+    } else {
+        pl.gg.splits = 1;
+        pl.gg.k_chunk = pl.gg.K;
+    }
+}
+
+// allow_ws = false plans without any workspace use: no operand copies and no split-K.
+int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
     Prob p;
     int st = normalise(d, p);
     if (st != MB_OK) return st;
@@ -467,30 +535,65 @@ int make_plan(const mb_gemm_desc *d, Plan &pl) {
 
     if (p.backend == MB_BACKEND_GENERIC) {
         plan_generic(p, pl);
+        if (!allow_ws) drop_splits(pl);
         return MB_OK;
     }
     const bool thin = p.M <= 16 || p.N <= 16;
     if (p.backend == MB_BACKEND_GEMV || (p.backend == MB_BACKEND_AUTO && thin)) {
-        if (plan_gemv(p, pl)) return MB_OK;
+        if (plan_gemv(p, pl)) {
+            if (!allow_ws) drop_splits(pl);
+            return MB_OK;
+        }
         if (p.backend == MB_BACKEND_GEMV) {
             // a gemv request whose matrix has no unit stride: generic kernel, same results
             plan_generic(p, pl);
+            if (!allow_ws) drop_splits(pl);
             return MB_OK;
         }
     }
     bool a_kc = false, b_kc = false;
-    if (mfma_layout_ok(p, a_kc, b_kc) && !(p.backend == MB_BACKEND_AUTO && p.M < 32 && p.N < 32)) {
+    const bool tiny = p.backend == MB_BACKEND_AUTO && p.M < 32 && p.N < 32;
+    if (mfma_layout_ok(p, a_kc, b_kc) && !tiny) {
         plan_mfma(p, pl, a_kc, b_kc);
+        if (!allow_ws) drop_splits(pl);
         return MB_OK;
     }
+    // operands the loaders cannot stream: copy them once into the workspace when the product
+    // is large enough for the matrix cores to repay the copy (2 x the operand bytes)
+    if (allow_ws && mfma_supported_dtype(p.dt) && !tiny &&
+        (p.backend == MB_BACKEND_AUTO || p.backend == MB_BACKEND_MATRIX || p.backend == MB_BACKEND_TILED) &&
+        (double)p.M * p.N * p.K * p.batch >= (double)(1 << 24)) {
+        Prob q = p;
+        Plan trial;
+        const int64_t pack_bytes = plan_packs(q, trial);
+        if (mfma_layout_ok(q, a_kc, b_kc)) {
+            pl.pack[0] = trial.pack[0];
+            pl.pack[1] = trial.pack[1];
+            pl.p = q;
+            plan_mfma(q, pl, a_kc, b_kc);
+            pl.split_off = pack_bytes;
+            pl.ws_bytes += pack_bytes;
+            return MB_OK;
+        }
+    }
     plan_generic(p, pl);
+    if (!allow_ws) drop_splits(pl);
     return MB_OK;
 }
 
 int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape) {
     hipError_t e = hipSuccess;
-    // workspace: fall back to a single K slice when the caller gave too little
     if (pl.ws_bytes > 0 && (!d->workspace || d->workspace_bytes < pl.ws_bytes)) return MB_ERR_WORKSPACE;
+    char *wsb = (char *)d->workspace;
+    for (int which = 0; which < 2; ++which) {
+        PackOp &pk = pl.pack[which];
+        if (!pk.on) continue;
+        pk.a.dst = wsb + pk.off;
+        e = launch_pack(pk.a, st);
+        if (e != hipSuccess) return MB_ERR_LAUNCH;
+        if (which == 0) pl.gg.a = pk.a.dst;
+        else pl.gg.b = pk.a.dst;
+    }
     switch (pl.family) {
         case MB_FAMILY_NONE:
             return MB_OK;
@@ -500,7 +603,7 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
         case MB_FAMILY_GENERIC:
         case MB_FAMILY_MFMA: {
             GemmArgs &g = pl.gg;
-            g.ws = d->workspace;
+            g.ws = wsb ? wsb + pl.split_off : nullptr;
             e = pl.family == MB_FAMILY_MFMA ? launch_mfma(pl.p.dt, pl.tile, pl.a_kc, pl.b_kc, g, st, shape)
                                             : launch_generic(pl.p.dt, g, st, shape);
             if (e == hipSuccess && g.splits > 1) e = launch_splitk_reduce(pl.p.dt, g, st);
@@ -537,20 +640,6 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
     return e == hipSuccess ? MB_OK : MB_ERR_LAUNCH;
 }
 
-// Drop split-K when no workspace was provided (correct results, less parallelism).
-void drop_split_without_ws(Plan &pl, const mb_gemm_desc *d) {
-    if (pl.ws_bytes <= 0) return;
-    if (d->workspace && d->workspace_bytes >= pl.ws_bytes) return;
-    pl.ws_bytes = 0;
-    if (pl.family == MB_FAMILY_GEMV_AXPY) {
-        pl.gv.splits = 1;
-        pl.gv.k_chunk = pl.gv.K;
-    } else {
-        pl.gg.splits = 1;
-        pl.gg.k_chunk = pl.gg.K;
-    }
-}
-
 }  // namespace
 
 extern "C" {
@@ -559,7 +648,12 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream) {
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
-    drop_split_without_ws(pl, desc);
+    if (pl.ws_bytes > 0 && (!desc->workspace || desc->workspace_bytes < pl.ws_bytes)) {
+        // not enough caller scratch: the plan that needs none (same results)
+        pl = Plan();
+        st = make_plan(desc, pl, false);
+        if (st != MB_OK) return st;
+    }
     return run_plan(pl, desc, (hipStream_t)stream, nullptr);
 }
 

@@ -388,3 +388,58 @@ def test_matrix_core_schedules(dev, dtype, tile, shape, layout):
     b = rand((K, N), dtype, g) if layout[1] == "r" else rand((N, K), dtype, g).t()
     got = mb.matmul(_to(a, dev), _to(b, dev), backend="mpp", tile=tile)
     assert_parity(got, a, b, tag=f"tile {tile} {dtype} {layout} {shape}")
+
+
+# ---- operands the matrix-core loaders cannot stream in place (copied into the workspace) ------
+
+def _offset_view(shape, dtype, g, offset, transpose=False, ld_pad=0):
+    """A matrix view at a storage offset and/or with a padded leading dimension."""
+    rows, cols = (shape[1], shape[0]) if transpose else shape
+    ld = cols + ld_pad
+    base = rand((offset + rows * ld,), dtype, g)
+    v = base[offset:].as_strided((rows, cols), (ld, 1))
+    return v.t() if transpose else v
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8, torch.uint8], ids=str)
+@pytest.mark.parametrize("case", ["offset17_a", "offset1_b", "odd_ld_a", "odd_k", "both_cm_offset",
+                                  "batched_offset"])
+def test_unaligned_operands(dev, dtype, case):
+    g = gen(17)
+    M, N, K = 384, 320, 512
+    if case == "offset17_a":
+        a, b = _offset_view((M, K), dtype, g, 17), rand((K, N), dtype, g)
+    elif case == "offset1_b":
+        a, b = rand((M, K), dtype, g), _offset_view((K, N), dtype, g, 1)
+    elif case == "odd_ld_a":
+        a, b = _offset_view((M, K), dtype, g, 0, ld_pad=3), rand((K, N), dtype, g)
+    elif case == "odd_k":
+        K = 517
+        a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    elif case == "both_cm_offset":
+        a = _offset_view((M, K), dtype, g, 5, transpose=True)
+        b = _offset_view((K, N), dtype, g, 3, transpose=True)
+    else:
+        Bb = 3
+        base = rand((9 + Bb * M * K,), dtype, g)
+        a = base[9:].view(Bb, M, K)
+        b = rand((Bb, K, N), dtype, g)
+        got = mb.bmm(_to(a, dev), _to(b, dev))
+        assert_parity(got, a, b, tag=f"unaligned {case} {dtype}")
+        return
+    got = mb.matmul(_to(a, dev), _to(b, dev))
+    plan = mb.kernels.plan(_to(a, dev), _to(b, dev))
+    assert plan["family"] == "mfma", plan
+    assert_parity(got, a, b, tag=f"unaligned {case} {dtype} {tuple(a.stride())} off {a.storage_offset()}")
+
+
+def test_unaligned_addmm_config3_offset(dev):
+    """BASELINE config 3 'offset' layout: a contiguous view at storage offset 17, with addmm."""
+    g = gen(3)
+    M, K, N = 1024, 2048, 768
+    flat = rand((17 + M * K,), torch.bfloat16, g)
+    a = flat[17:].view(M, K)
+    b = rand((K, N), torch.bfloat16, g)
+    bias = rand((N,), torch.bfloat16, g)
+    got = mb.addmm(bias.to(dev), _to(a, dev), b.to(dev), beta=0.5, alpha=2.0)
+    assert_parity(got, a, b, bias=bias, beta=0.5, alpha=2.0, tag="offset17 addmm")
