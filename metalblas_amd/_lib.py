@@ -208,19 +208,29 @@ def tile_candidates(desc: MbGemmDesc, cap: int = 16) -> list[tuple]:
     return [tuple(buf[8 * i: 8 * i + 8]) for i in range(n)]
 
 
-def run(desc: MbGemmDesc, device) -> None:
-    """Queue the product on torch's current stream of ``device``."""
-    lib = load()
+def workspace_bytes(desc: MbGemmDesc) -> int:
+    """Device scratch mb_gemm() needs for this descriptor."""
+    n = int(load().mb_gemm_workspace_bytes(ctypes.byref(desc)))
+    if n < 0:
+        check(n)
+    return n
+
+
+def launch(desc: MbGemmDesc, nbytes: int, device) -> None:
+    """Queue the product on torch's current stream of ``device`` (the current device) with
+    ``nbytes`` of workspace from torch's stream-ordered caching allocator."""
     ws = None
-    nbytes = int(lib.mb_gemm_workspace_bytes(ctypes.byref(desc)))
-    if nbytes < 0:
-        check(nbytes)
     if nbytes > 0:
         ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
-        desc.workspace = ctypes.c_void_p(ws.data_ptr())
+        desc.workspace = ws.data_ptr()
         desc.workspace_bytes = nbytes
-    stream = torch.cuda.current_stream(device).cuda_stream
-    status = lib.mb_gemm(ctypes.byref(desc), ctypes.c_void_p(stream))
-    check(status)
-    # ws is released to torch's caching allocator on the same stream: stream-ordered reuse
+    status = load().mb_gemm(ctypes.byref(desc), torch.cuda.current_stream().cuda_stream)
+    if status:
+        check(status)
+    # ws returns to torch's caching allocator; reuse is ordered on the same stream
     del ws
+
+
+def run(desc: MbGemmDesc, device) -> None:
+    """Queue the product on torch's current stream of ``device``."""
+    launch(desc, workspace_bytes(desc), device)

@@ -89,17 +89,49 @@ def _conj_split(t):
     return t, False
 
 
+# Descriptors already planned (and tuned) for a call signature: the dtype, sizes, strides,
+# pointer alignment classes, flags and scalars.  A hit skips descriptor construction and the
+# tuner; only the four data pointers change between calls.
+_DESC_CACHE: dict = {}
+_DESC_CACHE_CAP = 4096
+
+
+def _sig(t):
+    return None if t is None else (tuple(t.stride()), t.data_ptr() & 255)
+
+
 def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_a=False,
             conj_b=False, backend=_lib.BACKEND_AUTO, tile=None, swizzle_log=None):
     """Describe and queue one (batched) product; a/b/out/bias are 2-D or 3-D tensors."""
-    desc = _lib.make_desc(dtype, batch, M, N, K, _mat(a), _mat(b), _mat(out),
-                          _mat(bias) if bias is not None else None,
-                          conj_a=conj_a, conj_b=conj_b, epilogue=epilogue, backend=backend,
-                          tile=tile, swizzle_log=swizzle_log)
-    if backend == _lib.BACKEND_AUTO and tile is None:
-        _planner.tune(desc, a, b, out, bias)
-    with torch.cuda.device(out.device):
-        _lib.run(desc, out.device)
+    dev = out.device
+    key = (dtype, batch, M, N, K, _sig(a), _sig(b), _sig(out), _sig(bias), conj_a, conj_b,
+           epilogue, backend, tile if tile is None else tuple(tile), swizzle_log, dev.index,
+           _planner.enabled())
+    hit = _DESC_CACHE.get(key)
+    if hit is None:
+        desc = _lib.make_desc(dtype, batch, M, N, K, _mat(a), _mat(b), _mat(out),
+                              _mat(bias) if bias is not None else None,
+                              conj_a=conj_a, conj_b=conj_b, epilogue=epilogue, backend=backend,
+                              tile=tile, swizzle_log=swizzle_log)
+        if backend == _lib.BACKEND_AUTO and tile is None:
+            with torch.cuda.device(dev):
+                _planner.tune(desc, a, b, out, bias)
+        hit = (desc, _lib.workspace_bytes(desc))
+        if len(_DESC_CACHE) >= _DESC_CACHE_CAP:
+            _DESC_CACHE.clear()
+        _DESC_CACHE[key] = hit
+    template, ws_bytes = hit
+    desc = _lib.MbGemmDesc.from_buffer_copy(template)
+    desc.a.ptr = a.data_ptr()
+    desc.b.ptr = b.data_ptr()
+    desc.c.ptr = out.data_ptr()
+    if bias is not None:
+        desc.bias.ptr = bias.data_ptr()
+    if dev.index == torch.cuda.current_device():
+        _lib.launch(desc, ws_bytes, dev)
+    else:
+        with torch.cuda.device(dev):
+            _lib.launch(desc, ws_bytes, dev)
     return out
 
 
