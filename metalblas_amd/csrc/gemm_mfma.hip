@@ -19,6 +19,9 @@ hipError_t launch_f16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim
 hipError_t launch_f16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_bf16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_f16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_i8_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_i8_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_i8_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
 }  // namespace m16
 
 namespace {
@@ -31,13 +34,14 @@ constexpr TileEntry kTiles[] = {
     {256, 256, 2, 2, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0}, {128, 128, 2, 2, 0},
     {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},   {32, 32, 1, 1, 0},
 };
-// LDS-direct 16-bit family (mfma16.hpp): bf16 / fp16; sched 1 = the ping-pong kernel
+// LDS-direct family (mfma16.hpp): bf16 / fp16 / int8 / uint8; sched 1 = the ping-pong kernel
 constexpr TileEntry kTiles16[] = {
     {256, 256, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
     {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
 };
 
-bool is16(int dt) { return dt == BF16 || dt == F16; }
+// dtypes of the LDS-direct family
+bool is16(int dt) { return dt == BF16 || dt == F16 || dt == I8 || dt == U8; }
 
 bool in_table(const TileEntry *tb, int n, const MfmaTile &t) {
     for (int i = 0; i < n; ++i)
@@ -48,13 +52,13 @@ bool in_table(const TileEntry *tb, int n, const MfmaTile &t) {
 
 // The LDS-direct loads address each operand tile with 31-bit byte offsets from the tile's
 // first element; larger spans take the register-staged kernel.
-bool m16_offsets_fit(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g) {
+bool m16_offsets_fit(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, int es) {
     const int64_t lim = (int64_t)1 << 30;
     const int64_t lda = a_kc ? g.a_rs : g.a_cs, ldb = b_kc ? g.b_cs : g.b_rs;
-    const int64_t K = (int64_t)g.k_chunk + 64;
+    const int64_t K = (int64_t)g.k_chunk + 128 / es;
     const int64_t ea = a_kc ? (int64_t)t.bm * lda + K : K * lda + t.bm;
     const int64_t eb = b_kc ? (int64_t)t.bn * ldb + K : K * ldb + t.bn;
-    return ea * 2 < lim && eb * 2 < lim;
+    return ea * es < lim && eb * es < lim;
 }
 
 }  // namespace
@@ -85,22 +89,33 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
     dim3 grid(tiles, g.splits, g.batch < 65535 ? g.batch : 65535);
     if (shape) *shape = {grid, dim3(64 * t.wm * t.wn)};
     if (is16(dt) && !(t.bm == 32 && t.bn == 32)) {
-        if (m16_offsets_fit(t, a_kc, b_kc, g)) {
-            const bool whole = (g.k_chunk % 64) == 0 && (g.K % 64) == 0;
-            if (t.sched == 1)
-                return dt == BF16 ? m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st)
-                                  : m16::launch_f16_pp(!whole, a_kc, b_kc, g, grid, st);
+        const int es = dtype_size(dt), bk = 128 / es;
+        if (m16_offsets_fit(t, a_kc, b_kc, g, es)) {
+            const bool whole = (g.k_chunk % bk) == 0 && (g.K % bk) == 0;
+            if (t.sched == 1) {
+                if (dt == BF16) return m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st);
+                if (dt == F16) return m16::launch_f16_pp(!whole, a_kc, b_kc, g, grid, st);
+                return m16::launch_i8_pp(!whole, a_kc, b_kc, g, grid, st);   // int8 and uint8
+            }
             if (dt == BF16)
                 return whole ? m16::launch_bf16_kwhole(t, a_kc, b_kc, g, grid, st)
                              : m16::launch_bf16_ktail(t, a_kc, b_kc, g, grid, st);
-            return whole ? m16::launch_f16_kwhole(t, a_kc, b_kc, g, grid, st)
-                         : m16::launch_f16_ktail(t, a_kc, b_kc, g, grid, st);
+            if (dt == F16)
+                return whole ? m16::launch_f16_kwhole(t, a_kc, b_kc, g, grid, st)
+                             : m16::launch_f16_ktail(t, a_kc, b_kc, g, grid, st);
+            return whole ? m16::launch_i8_kwhole(t, a_kc, b_kc, g, grid, st)
+                         : m16::launch_i8_ktail(t, a_kc, b_kc, g, grid, st);
         }
         // very large leading dimensions: register-staged kernel with a compiled 4-wave tile
         MfmaTile v = in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t) ? t : MfmaTile{128, 128, 2, 2, 0};
         dim3 grid2(cdiv(g.M, v.bm) * cdiv(g.N, v.bn), g.splits, grid.z);
         if (shape) *shape = {grid2, dim3(64 * v.wm * v.wn)};
-        return dt == BF16 ? mfma::launch_bf16(v, a_kc, b_kc, g, grid2, st) : mfma::launch_f16(v, a_kc, b_kc, g, grid2, st);
+        switch (dt) {
+            case BF16: return mfma::launch_bf16(v, a_kc, b_kc, g, grid2, st);
+            case F16: return mfma::launch_f16(v, a_kc, b_kc, g, grid2, st);
+            case I8: return mfma::launch_i8(v, a_kc, b_kc, g, grid2, st);
+            default: return mfma::launch_u8(v, a_kc, b_kc, g, grid2, st);
+        }
     }
     switch (dt) {
         case BF16: return mfma::launch_bf16(t, a_kc, b_kc, g, grid, st);

@@ -391,7 +391,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const bool forced = p.tile[0] > 0 && p.tile[1] > 0;
     if (forced) {
         t = snap_tile(p.dt, p.tile);
-    } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16) {
+    } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8) {
         // Occupancy-aware cost model over the LDS-direct 16-bit tiles.  occ = workgroups per
         // CU (LDS and VGPR limited), eff = relative per-CU throughput at that occupancy,
         // measured on a bf16 8192^3 product on MI355X.  Time ~ rounds * occ * BM*BN / eff.

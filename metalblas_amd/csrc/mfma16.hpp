@@ -1,4 +1,9 @@
-// Matrix-core GEMM for 16-bit inputs (bf16 / fp16) on gfx950, fed by LDS-direct loads.
+// Matrix-core GEMM for 16-bit inputs (bf16 / fp16) and 8-bit integers (int8 / uint8) on
+// gfx950, fed by LDS-direct loads.  A stage is always 128 bytes of K per M/N index: 64 bf16 /
+// fp16 (v_mfma_f32_32x32x16, 4 k-steps of 16) or 128 int8 (v_mfma_i32_32x32x32_i8, 4 k-steps
+// of 32), so the LDS geometry, the swizzles of K-contiguous operands and the pipeline are
+// shared; only the transposing read of M/N-contiguous operands differs
+// (ds_read_b64_tr_b16 vs ds_read_b64_tr_b8).
 //
 // Differences from the register-staged matrix-core template (mfma_gemm.hpp):
 //   * Operand tiles go from global memory straight into LDS with buffer_load_dwordx4 ... lds
@@ -32,7 +37,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 #define MB_LDS __attribute__((address_space(3)))
 
 constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that is always out of range
@@ -65,34 +72,30 @@ __device__ __forceinline__ void pf_line(i32x4 rsrc, uint32_t lds_addr, uint32_t 
 }
 constexpr int kPfDist = 3;   // stages between a line's L2 prefetch and its LDS-direct load
 
-// Byte offset (from the operand tile's first element) of 128-byte line `idx` of one 64-deep
-// stage of a ROWS-wide operand tile, or kOOB.  K-contiguous operands have one line per row;
-// M/N-contiguous ones have ROWS * 2 / 128 lines per k.  Every stage has ROWS lines.
-template <int ROWS, bool KC>
+// Byte offset (from the operand tile's first element) of 128-byte line `idx` of one stage
+// (128 bytes of K) of a ROWS-wide operand tile with ES-byte elements, or kOOB.  K-contiguous
+// operands have one line per row; M/N-contiguous ones have ROWS * ES / 128 lines per k.
+// Every stage has ROWS lines.
+template <int ROWS, bool KC, int ES>
 __device__ __forceinline__ uint32_t pf_line_offset(int idx, int64_t ld, int rows_left, int k_left) {
     if constexpr (KC) {
         if (idx >= ROWS || idx >= rows_left) return kOOB;
-        return (uint32_t)((int64_t)idx * ld * 2);
+        return (uint32_t)((int64_t)idx * ld * ES);
     } else {
-        constexpr int LPR = ROWS * 2 / 128;
+        constexpr int LPR = ROWS * ES / 128;
+        constexpr int EPL = 128 / ES;   // elements per line
         const int r = idx / LPR, c = idx % LPR;
-        if (r >= 64 || r >= k_left || c * 64 >= rows_left) return kOOB;
-        return (uint32_t)(((int64_t)r * ld + c * 64) * 2);
+        if (r >= 128 / ES || r >= k_left || c * EPL >= rows_left) return kOOB;
+        return (uint32_t)(((int64_t)r * ld + c * EPL) * ES);
     }
 }
-// XCD-cooperative prefetch assignment.  The tiles that run together on one XCD form an
-// 8 (M) x 4 (N) block (tile_coords16 order), so each A stage is shared by 4 workgroups and
-// each B stage by 8: workgroup (tm, tn) prefetches quarter (tn % 4) of its A lines with
-// wave 0 and eighth (tm % 8) of its B lines with wave 1.  The assignment only steers which
-// lines reach L2 early; every wave issues exactly one prefetch per stage so the vmcnt
-// arithmetic stays uniform.
-template <int BM, int BN, bool A_KC, bool B_KC>
+template <int BM, int BN, bool A_KC, bool B_KC, int ES>
 __device__ __forceinline__ uint32_t pf_assign(int wave, int lane, int tm, int tn, int64_t lda, int64_t ldb,
                                               int rows_a, int rows_b, int k_left) {
     if (wave == 0 && lane < BM / 4)
-        return pf_line_offset<BM, A_KC>((tn & 3) * (BM / 4) + lane, lda, rows_a, k_left);
+        return pf_line_offset<BM, A_KC, ES>((tn & 3) * (BM / 4) + lane, lda, rows_a, k_left);
     if (wave == 1 && lane < BN / 8)
-        return pf_line_offset<BN, B_KC>((tm & 7) * (BN / 8) + lane, ldb, rows_b, k_left);
+        return pf_line_offset<BN, B_KC, ES>((tm & 7) * (BN / 8) + lane, ldb, rows_b, k_left);
     return kOOB;
 }
 
@@ -106,7 +109,12 @@ __device__ __forceinline__ i32x4 make_rsrc(const void *base) {
     return __builtin_bit_cast(i32x4, r);
 }
 
-template <class T> __device__ __forceinline__ void mma16(f32x16 &c, uint4 a, uint4 b);
+// Accumulator block of one 32 x 32 MFMA: fp32 for the float types, int32 (wrapping) for int8.
+template <class T> struct AccV { using type = f32x16; };
+template <> struct AccV<int8_t> { using type = i32x16; };
+template <> struct AccV<uint8_t> { using type = i32x16; };
+
+template <class T> __device__ __forceinline__ void mma16(typename AccV<T>::type &c, uint4 a, uint4 b);
 template <> __device__ __forceinline__ void mma16<bf16_t>(f32x16 &c, uint4 a, uint4 b) {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                 0, 0, 0);
@@ -115,12 +123,26 @@ template <> __device__ __forceinline__ void mma16<f16_t>(f32x16 &c, uint4 a, uin
     c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                0, 0);
 }
+// uint8 runs through the signed instruction: every operand is congruent to its signed
+// reinterpretation modulo 2^8, so the wrapped sums agree modulo 2^32 and the truncated
+// 8-bit results are identical.
+template <> __device__ __forceinline__ void mma16<int8_t>(i32x16 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0,
+                                              0, 0);
+}
+template <> __device__ __forceinline__ void mma16<uint8_t>(i32x16 &c, uint4 a, uint4 b) { mma16<int8_t>(c, a, b); }
 
 __device__ __forceinline__ int swz_k(int row) { return (row & 7) ^ ((row >> 3) & 3); }
-template <int CPR> __device__ __forceinline__ int swz_mn(int k) {
-    // {0, 4, 10, 14}[k & 3], limited to the chunks of one row
-    const int f = ((k & 1) << 2) | ((k & 2) ? 10 : 0);
-    return f & (CPR - 1);
+// Chunk swizzle of M/N-major rows.  16-bit: {0, 4, 10, 14}[k & 3]; 8-bit: 2 (k & 7), which
+// puts the 8 k-rows x 2 chunks that a 32-lane slice of one ds_read_b64_tr_b8 touches on 16
+// distinct 16-byte bank groups (for 256-byte rows).  Limited to the chunks of one row.
+template <int CPR, int ES> __device__ __forceinline__ int swz_mn(int k) {
+    if constexpr (ES == 2) {
+        const int f = ((k & 1) << 2) | ((k & 2) ? 10 : 0);
+        return f & (CPR - 1);
+    } else {
+        return (2 * (k & 7)) & (CPR - 1);
+    }
 }
 
 __device__ __forceinline__ MB_LDS char *lds_ptr(const char *p) { return (MB_LDS char *)(MB_LDS void *)p; }
@@ -128,14 +150,15 @@ __device__ __forceinline__ uint32_t lds_addr(const char *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_ptr(p));
 }
 
-// One operand tile: ROWS (M or N) x 64 k, 16-bit elements.
-template <int ROWS, int NW, bool KC> struct Tile16 {
+// One operand tile: ROWS (M or N) x 128 bytes of K (64 16-bit or 128 8-bit elements).
+template <int ROWS, int NW, bool KC, int ES = 2> struct Tile16 {
     static constexpr int BYTES = ROWS * 128;
     static constexpr int SEGS = BYTES / 1024;      // 1 KiB direct-load segments
     static constexpr int PER_WAVE = (SEGS + NW - 1) / NW;
-    static constexpr int RB = ROWS * 2;            // MN-major row bytes
+    static constexpr int RB = ROWS * ES;           // MN-major row bytes
     static constexpr int CPR = RB / 16;            // MN-major chunks per row
-    static_assert(ROWS % 32 == 0 && (KC || ROWS >= 64), "tile rows");
+    static constexpr int EPC = 16 / ES;            // elements per 16-byte chunk
+    static_assert(ROWS % 32 == 0 && (KC || RB >= (ES == 2 ? 128 : 64)), "tile rows");
 
     // Byte offset (relative to the resource base = element (row0, k0)) of the chunk a lane
     // loads for segment `seg`, or kOOB.
@@ -145,26 +168,34 @@ template <int ROWS, int NW, bool KC> struct Tile16 {
         if constexpr (KC) {
             const int r = byte >> 7, p = (byte >> 4) & 7;
             const int c = p ^ swz_k(r);
-            if (r >= rows_left || c * 8 >= k_left) return kOOB;
-            return (uint32_t)(((int64_t)r * ld + c * 8) * 2);
+            if (r >= rows_left || c * EPC >= k_left) return kOOB;
+            return (uint32_t)(((int64_t)r * ld + c * EPC) * ES);
         } else {
             const int k = byte / RB, p = (byte % RB) >> 4;
-            const int c = p ^ swz_mn<CPR>(k);
-            if (k >= k_left || c * 8 >= rows_left) return kOOB;
-            return (uint32_t)(((int64_t)k * ld + c * 8) * 2);
+            const int c = p ^ swz_mn<CPR, ES>(k);
+            if (k >= k_left || c * EPC >= rows_left) return kOOB;
+            return (uint32_t)(((int64_t)k * ld + c * EPC) * ES);
         }
     }
 
     // Lane-dependent LDS byte offset of the fragment of MFMA block `j` (32 rows) at k-step 0;
     // k-steps and blocks j' = j (mod 2 for KC) add compile-time constants.
+    //   16-bit transposing read: a 16-lane group reads 4 k-rows x 16 columns (lane L gives 4
+    //   columns of k-row L / 4) and returns column L's 4 k values to lane L.
+    //   8-bit transposing read: a 16-lane group reads 8 k-rows x 16 columns (lane L gives 8
+    //   columns of k-row L / 2) and returns column L's 8 k values to lane L.
     __device__ __forceinline__ static int frag_base(int row0, int lane, int j) {
         if constexpr (KC) {
             const int row = row0 + (lane & 31);
             return row * 128;   // chunk part is added per step (swizzle depends on lane only)
-        } else {
+        } else if constexpr (ES == 2) {
             const int kr = (lane & 15) >> 2;   // k row within the 4-row group
             const int col = row0 + 32 * j + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-            return (kr + 8 * (lane >> 5)) * RB + (((col >> 3) ^ swz_mn<CPR>(kr)) << 4) + ((col & 7) << 1);
+            return (kr + 8 * (lane >> 5)) * RB + (((col >> 3) ^ swz_mn<CPR, ES>(kr)) << 4) + ((col & 7) << 1);
+        } else {
+            const int kr = (lane & 15) >> 1;   // k row within the 8-row group
+            const int col = row0 + 32 * j + 16 * ((lane >> 4) & 1) + 8 * (lane & 1);
+            return (kr + 16 * (lane >> 5)) * RB + (((col >> 4) ^ swz_mn<CPR, ES>(kr)) << 4) + (col & 15);
         }
     }
 
@@ -177,10 +208,19 @@ template <int ROWS, int NW, bool KC> struct Tile16 {
             uint4 out;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                // k = 16 s + 8 (lane / 32) + 4 t + kr; the lane terms are folded into base
-                const int koff = (16 * s + 4 * t) * RB;
-                bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
-                uint2 u = __builtin_bit_cast(uint2, v);
+                uint2 u;
+                if constexpr (ES == 2) {
+                    // k = 16 s + 8 (lane / 32) + 4 t + kr; the lane terms are folded into base
+                    const int koff = (16 * s + 4 * t) * RB;
+                    bf16x4 v =
+                        __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
+                    u = __builtin_bit_cast(uint2, v);
+                } else {
+                    // k = 32 s + 16 (lane / 32) + 8 t + kr
+                    const int koff = (32 * s + 8 * t) * RB;
+                    i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2 *)(lds_ptr(lds) + base + koff));
+                    u = __builtin_bit_cast(uint2, v);
+                }
                 if (t == 0) {
                     out.x = u.x;
                     out.y = u.y;
@@ -215,8 +255,9 @@ __device__ __forceinline__ void tile_coords16(int pid, int tiles_m, int tiles_n,
 // nw + 32 i; lane l owns row (l % 32) and columns 8 (r / 4) + 4 (l / 32) + r % 4 of register r.
 // Split-K slices write fp32 partial planes; otherwise the (optional) epilogue and one rounding.
 template <class T, int TM, int TN>
-__device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN][TM], int mw, int nw, int bz,
-                                             int ks, int lane) {
+__device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>::type (&acc)[TN][TM], int mw,
+                                             int nw, int bz, int ks, int lane) {
+    using A = typename Tr<T>::acc;   // fp32, or the unsigned 32-bit wrapping accumulator
     // keep the store addressing from being hoisted above the main loop (where its 64-bit
     // addresses would be live across the loop and spill)
     asm volatile("" : "+s"(mw), "+s"(nw));
@@ -224,7 +265,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN
     const int nsub = 4 * (lane >> 5);
     T *Cb = (T *)g.c + bz * g.c_bs;
     if (g.splits > 1) {
-        float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
+        A *ws = (A *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
         const bool vec = (g.N & 3) == 0;
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -232,17 +273,21 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN
             for (int j = 0; j < TM; ++j) {
                 const int gm = mw + j * 32 + mrow;
                 if (gm >= g.M) continue;
-                float *row = ws + (int64_t)gm * g.N;
+                A *row = ws + (int64_t)gm * g.N;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int gn = nw + i * 32 + 8 * q + nsub;
                     if (vec && gn + 3 < g.N) {
-                        *(float4 *)(row + gn) = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1],
-                                                            acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+                        A o[4];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) o[r] = (A)acc[i][j][4 * q + r];
+                        uint4 u;
+                        __builtin_memcpy(&u, o, 16);
+                        *(uint4 *)(row + gn) = u;
                     } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            if (gn + r < g.N) row[gn + r] = acc[i][j][4 * q + r];
+                            if (gn + r < g.N) row[gn + r] = (A)acc[i][j][4 * q + r];
                     }
                 }
             }
@@ -261,9 +306,15 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN
                         T o[4];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
-                        uint2 u;
-                        __builtin_memcpy(&u, o, 8);
-                        *(uint2 *)(row + gn) = u;
+                        if constexpr (sizeof(T) == 2) {
+                            uint2 u;
+                            __builtin_memcpy(&u, o, 8);
+                            *(uint2 *)(row + gn) = u;
+                        } else {
+                            uint32_t u;
+                            __builtin_memcpy(&u, o, 4);
+                            *(uint32_t *)(row + gn) = u;
+                        }
                     } else {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
@@ -285,7 +336,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN
                     for (int r = 0; r < 4; ++r) {
                         const int n = gn + r;
                         if (n < g.N)
-                            store_out<T>(g, Cb + gm * g.c_rs + n * g.c_cs, acc[i][j][4 * q + r],
+                            store_out<T>(g, Cb + gm * g.c_rs + n * g.c_cs, (A)acc[i][j][4 * q + r],
                                          bz * g.bias_bs + gm * g.bias_rs + n * g.bias_cs);
                     }
                 }
@@ -293,16 +344,17 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, f32x16 (&acc)[TN
     }
 }
 
-// KTAIL: some K slice ends inside a 64-wide stage (its last stage is zero-filled past the
+// KTAIL: some K slice ends inside a stage (its last stage is zero-filled past the
 // edge).  Without it the main loop carries no edge logic.
 template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL>
 __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     constexpr int NW = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int BK = 64;
-    using TA = Tile16<BM, NW, A_KC>;
-    using TB = Tile16<BN, NW, B_KC>;
+    constexpr int ES = sizeof(T);
+    constexpr int BK = 128 / ES;   // elements of K per stage
+    using TA = Tile16<BM, NW, A_KC, ES>;
+    using TB = Tile16<BN, NW, B_KC, ES>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
     static_assert(TM >= 1 && TN >= 1, "wave tile");
     // LDS read instructions per k-step (a transposing fragment takes two)
@@ -330,10 +382,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     const int64_t lda = A_KC ? g.a_rs : g.a_cs;
     const int64_t ldb = B_KC ? g.b_cs : g.b_rs;
     const int rows_a = g.M - m0, rows_b = g.N - n0;
-    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * 2);
-    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * 2);
+    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * ES);
+    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * ES);
     // this lane's L2 prefetch line (full stages; the K-edge stage recomputes it)
-    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
+    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
     const bool pf_on_a = wave == 0;
 
     // loop-invariant per-lane source offsets (full stages)
@@ -396,17 +448,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
             }
             const int kp = kt + kPfDist;
             const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
-                              : pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+                              : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
             pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
         };
 
-        f32x16 acc[TN][TM];
+        typename AccV<T>::type acc[TN][TM];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
         uint4 fa[2][TM], fb[2][TN];
         auto read_frags = [&](const char *cur, int s, int slot) {
@@ -462,7 +514,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 
 // Ping-pong schedule of the 256 x 256 tile with 8 waves, two per SIMD (waves w and w + 4
 // share SIMD w % 4).  The waves form two groups, 0..3 and 4..7, that alternate between a
-// memory phase (all LDS fragment reads of one 64-deep stage into registers, plus this wave's
+// memory phase (all LDS fragment reads of one stage into registers, plus this wave's
 // share of the LDS-direct prefetch) and a compute phase (the stage's 32 MFMAs back to back,
 // every operand already in registers).  Group 1 runs one phase behind group 0, so on each
 // SIMD one wave keeps the matrix core busy while the other feeds it; a workgroup barrier
@@ -481,9 +533,10 @@ template <class T, bool A_KC, bool B_KC, bool KTAIL>
 __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     constexpr int BM = 256, BN = 256, WM = 2, NW = 8;
     constexpr int WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
-    constexpr int BK = 64, KSTEPS = BK / 16;
-    using TA = Tile16<BM, NW, A_KC>;
-    using TB = Tile16<BN, NW, B_KC>;
+    constexpr int ES = sizeof(T);
+    constexpr int BK = 128 / ES, KSTEPS = 4;
+    using TA = Tile16<BM, NW, A_KC, ES>;
+    using TB = Tile16<BN, NW, B_KC, ES>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
 
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
@@ -508,10 +561,10 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     const int64_t lda = A_KC ? g.a_rs : g.a_cs;
     const int64_t ldb = B_KC ? g.b_cs : g.b_rs;
     const int rows_a = g.M - m0, rows_b = g.N - n0;
-    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * 2);
-    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * 2);
+    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * ES);
+    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * ES);
     // this lane's L2 prefetch line (full stages; the K-edge stage recomputes it)
-    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
+    const uint32_t pfoff = pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, BK);
     const bool pf_on_a = wave == 0;
 
     uint32_t offa[TA::PER_WAVE], offb[TB::PER_WAVE];
@@ -552,17 +605,17 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             }
             const int kp = kt + kPfDist;
             const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
-                              : pf_assign<BM, BN, A_KC, B_KC>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+                              : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
             pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
         };
 
-        f32x16 acc[TN][TM];
+        typename AccV<T>::type acc[TN][TM];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
         uint4 fa[KSTEPS][TM], fb[KSTEPS][TN];
         auto read_stage = [&](int kt) {

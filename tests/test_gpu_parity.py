@@ -375,7 +375,7 @@ def test_gemv_config2_sizes(dev, n):
 
 # ---- every compiled 16-bit matrix-core schedule, forced, on edge shapes and all layouts ---------
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.int8, torch.uint8], ids=str)
 @pytest.mark.parametrize("tile", [(256, 256, 64, 2, 4, 1), (256, 256, 64, 2, 4, 2), (256, 256, 64, 2, 2, 1),
                                   (128, 128, 64, 2, 2, 1), (64, 64, 64, 2, 2, 1)], ids=str)
 @pytest.mark.parametrize("shape", [(256, 256, 64), (513, 257, 129), (1000, 700, 1000), (512, 768, 4160),
@@ -443,3 +443,24 @@ def test_unaligned_addmm_config3_offset(dev):
     bias = rand((N,), torch.bfloat16, g)
     got = mb.addmm(bias.to(dev), _to(a, dev), b.to(dev), beta=0.5, alpha=2.0)
     assert_parity(got, a, b, bias=bias, beta=0.5, alpha=2.0, tag="offset17 addmm")
+
+
+@pytest.mark.parametrize("dtype", [torch.int8, torch.uint8], ids=str)
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+@pytest.mark.parametrize("tile", [None, (256, 256, 64, 2, 4, 2), (128, 128, 64, 2, 2, 1)], ids=str)
+def test_int8_full_range(dev, dtype, layout, tile):
+    """Full-range 8-bit operands through the int8 matrix cores: signed and unsigned values,
+    products wrapping modulo 2^8 on the store, and the fused integer epilogue."""
+    g = gen(88)
+    M, N, K = 512, 384, 1152
+    lo, hi = (-128, 128) if dtype is torch.int8 else (0, 256)
+    def full(shape):
+        return torch.randint(lo, hi, shape, generator=g, dtype=torch.int64).to(dtype)
+    a = full((M, K)) if layout[0] == "r" else full((K, M)).t()
+    b = full((K, N)) if layout[1] == "r" else full((N, K)).t()
+    kw = {} if tile is None else {"backend": "mpp", "tile": tile}
+    got = mb.matmul(_to(a, dev), _to(b, dev), **kw)
+    assert_parity(got, a, b, tag=f"int8 full {dtype} {layout} {tile}")
+    bias = full((N,))
+    got = mb.addmm(bias.to(dev), _to(a, dev), _to(b, dev), beta=3, alpha=-5)
+    assert_parity(got, a, b, bias=bias, beta=3, alpha=-5, tag=f"int8 addmm {dtype} {layout}")
