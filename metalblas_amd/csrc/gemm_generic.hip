@@ -177,12 +177,52 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
     }
 }
 
+// Bhat expansion (CplxExpandArgs): thread per (n, k pair-block) writes the two K-adjacent
+// pairs of Bhat's columns 2n and 2n + 1; the padding k' in [2K, ld) is zero-filled.
+template <class R>
+__global__ __launch_bounds__(256) void k_cplx_expand(CplxExpandArgs a) {
+    const int64_t kp = a.ld / 2;   // complex k positions per Bhat column, padding included
+    const int64_t total = (int64_t)a.N * kp;
+    const R sa = a.neg_a ? R(-1.f) : R(1.f), sb = a.neg_b ? R(-1.f) : R(1.f);
+    for (int64_t bz = blockIdx.y; bz < a.batch; bz += gridDim.y) {
+        const R *src = (const R *)a.b + 2 * bz * a.b_bs;
+        R *dst = (R *)a.dst + bz * a.d_bs;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+            const int64_t n = i / kp, k = i % kp;
+            R re = R(0.f), im = R(0.f);
+            if (k < a.K) {
+                const R *e = src + 2 * (k * a.b_rs + n * a.b_cs);
+                re = e[0];
+                im = e[1];
+            }
+            R *c0 = dst + (2 * n) * a.ld + 2 * k;        // column 2n: (re, -sa sb im)
+            R *c1 = dst + (2 * n + 1) * a.ld + 2 * k;    // column 2n+1: (sb im, sa re)
+            c0[0] = re;
+            c0[1] = -(sa * sb) * im;
+            c1[0] = sb * im;
+            c1[1] = sa * re;
+        }
+    }
+}
+
 inline int elementwise_blocks(int64_t total) {
     int64_t b = (total + 255) / 256;
     return (int)(b < 65536 ? (b < 1 ? 1 : b) : 65536);
 }
 
 }  // namespace
+
+hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st) {
+    const int64_t total = (int64_t)a.N * (a.ld / 2);
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    dim3 grid((unsigned)(blocks < 1 ? 1 : blocks), (unsigned)(a.batch < 65535 ? a.batch : 65535));
+    if (a.half)
+        hipLaunchKernelGGL(k_cplx_expand<f16_t>, grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_cplx_expand<float>, grid, dim3(256), 0, st, a);
+    return hipGetLastError();
+}
 
 hipError_t launch_pack(const PackArgs &a, hipStream_t st) {
     const int64_t inner_n = a.contig_cols ? a.cols_p : a.rows_p;

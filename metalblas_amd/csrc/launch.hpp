@@ -90,7 +90,24 @@ struct PackArgs {
     int32_t es;            // element bytes: 1, 2, 4 or 8
 };
 
+// Complex product as a real one: C (M x N complex) = A (M x K complex) @ B (K x N complex) is
+// the real product Chat (M x 2N) = Ahat (M x 2K) @ Bhat (2K x 2N), where Ahat is A's
+// interleaved (re, im) storage read as a real matrix and Bhat expands each element b of B
+// into the 2 x 2 block [[re b, s_b im b], [-s_a s_b im b, s_a re b]] (s = -1 for a
+// conjugated operand).  Bhat is written K-contiguous: element (k', n') at dst[n' * ld + k'],
+// zero-padded for k' in [2K, ld).
+struct CplxExpandArgs {
+    const void *b;
+    int64_t b_rs, b_cs, b_bs;   // complex element strides of B
+    void *dst;
+    int64_t ld, d_bs;           // real element strides of Bhat
+    int32_t K, N, batch;
+    int32_t neg_a, neg_b;       // conj(A), conj(B)
+    int32_t half;               // 1: complex32 (fp16 parts), 0: complex64 (fp32 parts)
+};
+
 // gemm_generic.hip
+hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st);
 hipError_t launch_pack(const PackArgs &a, hipStream_t st);
 hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);

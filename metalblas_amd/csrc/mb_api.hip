@@ -56,6 +56,13 @@ struct Plan {
     Prob p;
     PackOp pack[2];           // A, B
     int64_t split_off = 0;    // workspace byte offset of the split-K partial planes
+    // complex product run as the real product M x 2N x 2K (CplxExpandArgs)
+    bool cplx = false;
+    CplxExpandArgs cx;        // B expansion (dst set at run time)
+    int64_t cx_off = 0;
+    bool cplx_reduce = false; // real GEMM writes fp32 planes; a complex reduction applies the
+    GemmArgs cr;              // epilogue and the output strides (ws set at run time)
+    int cdt = 0;              // the complex dtype
     // GEMV
     GemvArgs gv;
     bool gemv_dot = false;
@@ -512,6 +519,109 @@ void drop_splits(Plan &pl) {
     }
 }
 
+// Complex GEMM on the real matrix cores: C = A @ B as the real product of A's interleaved
+// storage (M x 2K) with B expanded into 2 x 2 real blocks (2K x 2N, CplxExpandArgs), i.e. the
+// four real products P = Re A Re B, Q = Im A Im B, S = Re A Im B, T = Im A Re B of
+// metalblas/complex_dispatch.py:69-81 fused into one GEMM whose output columns interleave
+// Re C = P - Q and Im C = S + T (shaders/complex_pack.h:41-42).  Conjugation becomes signs in
+// the expansion.  complex64 runs on the fp32 matrix cores, complex32 on fp16 ones (fp32
+// accumulation).  Without an epilogue and with row-contiguous C the real GEMM writes C
+// directly; otherwise it writes fp32 planes and the split-K reduction, run as complex,
+// applies alpha/beta (shaders/complex_pack.h:43-58) and C's strides.
+bool plan_complex(const Prob &p, Plan &pl) {
+    const bool c64 = p.dt == MB_DTYPE_C64;
+    const int res = c64 ? 4 : 2;   // real element bytes
+    const int E = 16 / res;
+    const char *placeholder = (const char *)(uintptr_t)4096;
+    int64_t ws = 0;
+    Prob q = p;
+    q.dt = c64 ? F32 : F16;
+    q.N = 2 * p.N;
+    q.K = 2 * p.K;
+    q.conj_a = q.conj_b = 0;
+    q.epilogue = 0;
+    q.beta_nz = 0;
+    q.alpha_nz = 1;
+    q.bias = {nullptr, 0, 0, 0};
+    q.a_padded = q.b_padded = false;
+    // A: the interleaved storage read as a real K-contiguous matrix, or a complex copy
+    bool view_ok = p.a.cs == 1;
+    if (view_ok) {
+        q.a = {p.a.ptr, 2 * p.a.rs, 1, 2 * p.a.bs};
+        view_ok = operand_ok(q.a, 1, true, q);
+    }
+    if (!view_ok) {
+        PackOp &pk = pl.pack[0];
+        PackArgs &a = pk.a;
+        memset(&a, 0, sizeof(a));
+        const int64_t cols_p = (p.K + E / 2 - 1) / (E / 2) * (E / 2);   // real row length % E == 0
+        a.rows = a.rows_p = (int)p.M;
+        a.cols = (int)p.K;
+        a.cols_p = (int)cols_p;
+        a.contig_cols = 1;
+        a.batch = p.a.bs == 0 ? 1 : (int)p.batch;
+        a.src = p.a.ptr;
+        a.s_rs = p.a.rs; a.s_cs = p.a.cs; a.s_bs = p.a.bs;
+        a.d_rs = cols_p; a.d_cs = 1;
+        a.d_bs = p.a.bs == 0 ? 0 : p.M * cols_p;
+        a.es = dtype_size(p.dt);
+        pk.on = true;
+        pk.off = ws;
+        ws += (p.M * cols_p * a.batch * a.es + 255) / 256 * 256;
+        q.a = {placeholder, 2 * cols_p, 1, 2 * a.d_bs};
+        q.a_padded = true;
+    }
+    // B: expanded into the workspace, K-contiguous, K zero-padded to a 16-byte multiple
+    CplxExpandArgs &cx = pl.cx;
+    memset(&cx, 0, sizeof(cx));
+    const int64_t ldb = (2 * p.K + E - 1) / E * E;
+    cx.b = p.b.ptr;
+    cx.b_rs = p.b.rs; cx.b_cs = p.b.cs; cx.b_bs = p.b.bs;
+    cx.ld = ldb;
+    cx.K = (int)p.K;
+    cx.N = (int)p.N;
+    cx.batch = p.b.bs == 0 ? 1 : (int)p.batch;
+    cx.d_bs = p.b.bs == 0 ? 0 : 2 * p.N * ldb;
+    cx.neg_a = p.conj_a;
+    cx.neg_b = p.conj_b;
+    cx.half = !c64;
+    pl.cx_off = ws;
+    ws += (2 * p.N * ldb * cx.batch * res + 255) / 256 * 256;
+    q.b = {placeholder, 1, ldb, cx.d_bs};
+    q.b_padded = true;
+    // C: written directly when the real view is plain, else fp32 planes + complex reduction
+    const bool direct = !p.epilogue && p.c.cs == 1;
+    q.c = direct ? Operand{p.c.ptr, 2 * p.c.rs, 1, 2 * p.c.bs} : Operand{placeholder, q.N, 1, p.M * q.N};
+    bool a_kc = false, b_kc = false;
+    if (!mfma_layout_ok(q, a_kc, b_kc)) {
+        pl.pack[0] = PackOp();
+        return false;
+    }
+    plan_mfma(q, pl, a_kc, b_kc);
+    GemmArgs &g = pl.gg;
+    pl.split_off = ws;
+    if (direct) {
+        pl.ws_bytes += ws;   // split-K planes, if any, after the copies
+    } else {
+        g.planes = 1;
+        pl.ws_bytes = ws + (int64_t)g.splits * p.batch * p.M * q.N * 4;
+        GemmArgs &r = pl.cr;
+        memset(&r, 0, sizeof(r));
+        r.c = (void *)p.c.ptr;
+        r.bias = p.bias.ptr;
+        r.M = (int)p.M; r.N = (int)p.N; r.batch = (int)p.batch;
+        r.c_rs = p.c.rs; r.c_cs = p.c.cs; r.c_bs = p.c.bs;
+        r.bias_rs = p.bias.rs; r.bias_cs = p.bias.cs; r.bias_bs = p.bias.bs;
+        r.epilogue = p.epilogue; r.beta_nz = p.beta_nz; r.alpha_nz = p.alpha_nz;
+        r.s = p.s;
+        pl.cplx_reduce = true;
+    }
+    pl.cplx = true;
+    pl.cdt = p.dt;
+    pl.p = q;
+    return true;
+}
+
 // allow_ws = false plans without any workspace use: no operand copies and no split-K.
 int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
     Prob p;
@@ -553,6 +663,11 @@ int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
     }
     bool a_kc = false, b_kc = false;
     const bool tiny = p.backend == MB_BACKEND_AUTO && p.M < 32 && p.N < 32;
+    if ((p.dt == MB_DTYPE_C64 || p.dt == MB_DTYPE_C32) && allow_ws && !tiny &&
+        (p.backend == MB_BACKEND_AUTO || p.backend == MB_BACKEND_MATRIX || p.backend == MB_BACKEND_TILED) &&
+        (double)p.M * p.N * p.K * p.batch >= (double)(1 << 22)) {
+        if (plan_complex(p, pl)) return MB_OK;
+    }
     if (mfma_layout_ok(p, a_kc, b_kc) && !tiny) {
         plan_mfma(p, pl, a_kc, b_kc);
         if (!allow_ws) drop_splits(pl);
@@ -603,10 +718,23 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
         case MB_FAMILY_GENERIC:
         case MB_FAMILY_MFMA: {
             GemmArgs &g = pl.gg;
+            if (pl.cplx) {
+                pl.cx.dst = wsb + pl.cx_off;
+                e = launch_cplx_expand(pl.cx, st);
+                if (e != hipSuccess) break;
+                g.b = pl.cx.dst;
+            }
             g.ws = wsb ? wsb + pl.split_off : nullptr;
             e = pl.family == MB_FAMILY_MFMA ? launch_mfma(pl.p.dt, pl.tile, pl.a_kc, pl.b_kc, g, st, shape)
                                             : launch_generic(pl.p.dt, g, st, shape);
-            if (e == hipSuccess && g.splits > 1) e = launch_splitk_reduce(pl.p.dt, g, st);
+            if (e != hipSuccess) break;
+            if (pl.cplx_reduce) {
+                pl.cr.ws = g.ws;
+                pl.cr.splits = g.splits;
+                e = launch_splitk_reduce(pl.cdt, pl.cr, st);
+            } else if (g.splits > 1) {
+                e = launch_splitk_reduce(pl.p.dt, g, st);
+            }
             break;
         }
         case MB_FAMILY_GEMV_DOT:

@@ -205,6 +205,8 @@ struct GemmArgs {
     int32_t swz;         // tile-order group log2
     int32_t nv;          // GEMV families: number of vectors (thin dim)
     int32_t vec_ok;      // GEMV families: vectorised loads allowed
+    int32_t planes;      // write accumulator planes to ws even with one K slice (a later
+                         // reduction kernel finishes the output)
     EpiScalars s;
 };
 

@@ -264,7 +264,7 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
     const int mrow = lane & 31;
     const int nsub = 4 * (lane >> 5);
     T *Cb = (T *)g.c + bz * g.c_bs;
-    if (g.splits > 1) {
+    if (g.splits > 1 || g.planes) {
         A *ws = (A *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
         const bool vec = (g.N & 3) == 0;
 #pragma unroll

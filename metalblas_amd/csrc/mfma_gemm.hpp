@@ -321,7 +321,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm_mfma(GemmArgs g) {
         const int mrow = lane & 31;
         const int nsub = 4 * (lane >> 5);
         T *Cb = (T *)g.c + bz * g.c_bs;
-        const bool split = g.splits > 1;
+        const bool split = g.splits > 1 || g.planes;
         using AccT = typename Tr<T>::acc;
 #pragma unroll
         for (int i = 0; i < TN; ++i)

@@ -464,3 +464,42 @@ def test_int8_full_range(dev, dtype, layout, tile):
     bias = full((N,))
     got = mb.addmm(bias.to(dev), _to(a, dev), _to(b, dev), beta=3, alpha=-5)
     assert_parity(got, a, b, bias=bias, beta=3, alpha=-5, tag=f"int8 addmm {dtype} {layout}")
+
+
+# ---- complex products on the real matrix cores (expanded B, interleaved A) --------------------
+
+@pytest.mark.parametrize("dtype", [torch.complex64, torch.complex32], ids=str)
+@pytest.mark.parametrize("conj", ["none", "a", "b", "ab"])
+@pytest.mark.parametrize("layout", ["rr", "cr", "rc", "cc"])
+def test_complex_matrix_cores(dev, dtype, conj, layout):
+    g = gen(33)
+    M, N, K = 320, 288, 260
+    a = rand((M, K), dtype, g) if layout[0] == "r" else rand((K, M), dtype, g).t()
+    b = rand((K, N), dtype, g) if layout[1] == "r" else rand((N, K), dtype, g).t()
+    if "a" in conj:
+        a = a.conj()
+    if "b" in conj:
+        b = b.conj()
+    got = mb.matmul(_to(a, dev), _to(b, dev))
+    assert mb.kernels.plan(_to(a, dev).resolve_conj(), _to(b, dev).resolve_conj())["family"] == "mfma"
+    assert_parity(got, a, b, tag=f"complex mfma {dtype} conj={conj} {layout}")
+
+
+@pytest.mark.parametrize("dtype", [torch.complex64, torch.complex32], ids=str)
+def test_complex_matrix_cores_fused(dev, dtype):
+    """Complex epilogue through the complex reduction, column-major output, odd K, batches."""
+    g = gen(34)
+    M, N, K = 256, 320, 257
+    a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    bias = rand((N,), dtype, g)
+    beta, alpha = complex(0.5, -1.0), complex(2.0, 0.25)
+    got = mb.addmm(bias.to(dev), a.to(dev), b.to(dev), beta=beta, alpha=alpha)
+    assert_parity(got, a, b, bias=bias, beta=beta, alpha=alpha, tag=f"complex addmm {dtype}")
+    out = torch.empty(N, M, dtype=dtype, device=dev).t()
+    mb.matmul(a.to(dev), b.to(dev), out=out)
+    assert_parity(out, a, b, tag=f"complex cm out {dtype}")
+    a3, b3 = rand((3, M, K), dtype, g), rand((3, K, N), dtype, g)
+    assert_parity(mb.bmm(a3.to(dev), b3.to(dev)), a3, b3, tag=f"complex bmm {dtype}")
+    bb = rand((K, N), dtype, g)
+    got = mb.matmul(a3.to(dev), bb.to(dev))
+    assert_parity(got, a3, bb.expand(3, K, N), tag=f"complex broadcast {dtype}")
