@@ -256,6 +256,14 @@ def _matmul_nd(a, b, out=None):
         b3 = b.expand(*batch, K, N).reshape(size, K, N)
         result = bmm(a3, b3).reshape(*batch, M, N)
     else:
+        if (out is not None and (a_vec or b_vec) and out.dtype == a.dtype == b.dtype
+                and out.device == a.device):
+            # a 1-D result: write straight into out's (M, N) view, no temporary + copy
+            o2 = out.unsqueeze(0) if a_vec and not b_vec else out.unsqueeze(-1) if b_vec and not a_vec \
+                else out.reshape(1, 1)
+            if o2.shape == (M, N) and o2.data_ptr() == out.data_ptr():
+                matmul(a, b, out=o2)
+                return out
         result = matmul(a, b)
     if a_vec:
         result = result.squeeze(-2)
