@@ -9,6 +9,8 @@
 // 64x64 output tile, 256 threads as 16x16, 4x4 accumulators per thread, BK = 16.
 #include "launch.hpp"
 
+#include <type_traits>
+
 namespace mb {
 
 namespace {
@@ -151,6 +153,50 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(GemmArgs g) {
     }
 }
 
+// The same reduction for fp32 partials with N % 4 == 0: each thread sums 4 consecutive outputs
+// of one row with 16-byte loads (same summation order per output as k_splitk_reduce).
+template <class T, int TPO>
+__global__ __launch_bounds__(256) void k_splitk_reduce4(GemmArgs g) {
+    constexpr int OPB = 256 / TPO;   // 4-output groups per block iteration
+    __shared__ float4 part[TPO][OPB];
+    const int64_t plane = (int64_t)g.batch * g.M * g.N;
+    const int64_t groups = plane / 4;
+    const float4 *ws = (const float4 *)g.ws;
+    const int sub = threadIdx.x / OPB, oi = threadIdx.x % OPB;
+    auto add = [](float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); };
+    for (int64_t base = (int64_t)blockIdx.x * OPB; base < groups; base += (int64_t)gridDim.x * OPB) {
+        const int64_t i = base + oi;
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0, v2 = v0, v3 = v0;
+        if (i < groups) {
+            int s = sub;
+            for (; s + 3 * TPO < g.splits; s += 4 * TPO) {
+                v0 = add(v0, ws[(int64_t)s * groups + i]);
+                v1 = add(v1, ws[(int64_t)(s + TPO) * groups + i]);
+                v2 = add(v2, ws[(int64_t)(s + 2 * TPO) * groups + i]);
+                v3 = add(v3, ws[(int64_t)(s + 3 * TPO) * groups + i]);
+            }
+            for (; s < g.splits; s += TPO) v0 = add(v0, ws[(int64_t)s * groups + i]);
+        }
+        part[sub][oi] = add(add(v0, v1), add(v2, v3));
+        __syncthreads();
+        if (sub == 0 && i < groups) {
+            float4 v = part[0][oi];
+#pragma unroll
+            for (int q = 1; q < TPO; ++q) v = add(v, part[q][oi]);
+            const int64_t e = 4 * i;
+            const int64_t bz = e / ((int64_t)g.M * g.N);
+            const int64_t r = e % ((int64_t)g.M * g.N);
+            const int64_t m = r / g.N, n = r % g.N;   // n % 4 == 0: the 4 outputs share row m
+            T *c = (T *)g.c + bz * g.c_bs + m * g.c_rs;
+            const int64_t bo = bz * g.bias_bs + m * g.bias_rs;
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) store_out<T>(g, c + (n + q) * g.c_cs, vv[q], bo + (n + q) * g.bias_cs);
+        }
+        __syncthreads();
+    }
+}
+
 // Operand copy (PackArgs): each thread writes 4 consecutive elements along the destination's
 // contiguous dimension (coalesced stores); source reads follow the source strides.  The grid
 // is x: inner chunks, y: outer index (grid-stride), z: batch (grid-stride).
@@ -260,12 +306,27 @@ hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st) {
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st) {
     const int64_t plane = (int64_t)g.batch * g.M * g.N;
     // threads per output: enough that a block covers ~8 planes per thread
-    const int tpo = g.splits >= 64 ? 8 : (g.splits >= 16 ? 4 : (g.splits >= 4 ? 2 : 1));
+    const int tpo = g.splits >= 128 ? 16 : g.splits >= 64 ? 8 : (g.splits >= 16 ? 4 : (g.splits >= 4 ? 2 : 1));
     const int64_t opb = 256 / tpo;
     int64_t blocks = (plane + opb - 1) / opb;
     if (blocks > 8192) blocks = 8192;
     return with_dtype(dt, [&]<class T>() {
+        if constexpr (std::is_same_v<typename Tr<T>::acc, float>) {
+            if (g.N % 4 == 0 && ((uintptr_t)g.ws & 15) == 0) {
+                int64_t b4 = (plane / 4 + opb - 1) / opb;
+                if (b4 > 8192) b4 = 8192;
+                switch (tpo) {
+                    case 16: hipLaunchKernelGGL((k_splitk_reduce4<T, 16>), dim3(b4), dim3(256), 0, st, g); break;
+                    case 8: hipLaunchKernelGGL((k_splitk_reduce4<T, 8>), dim3(b4), dim3(256), 0, st, g); break;
+                    case 4: hipLaunchKernelGGL((k_splitk_reduce4<T, 4>), dim3(b4), dim3(256), 0, st, g); break;
+                    case 2: hipLaunchKernelGGL((k_splitk_reduce4<T, 2>), dim3(b4), dim3(256), 0, st, g); break;
+                    default: hipLaunchKernelGGL((k_splitk_reduce4<T, 1>), dim3(b4), dim3(256), 0, st, g); break;
+                }
+                return hipGetLastError();
+            }
+        }
         switch (tpo) {
+            case 16: hipLaunchKernelGGL((k_splitk_reduce<T, 16>), dim3(blocks), dim3(256), 0, st, g); break;
             case 8: hipLaunchKernelGGL((k_splitk_reduce<T, 8>), dim3(blocks), dim3(256), 0, st, g); break;
             case 4: hipLaunchKernelGGL((k_splitk_reduce<T, 4>), dim3(blocks), dim3(256), 0, st, g); break;
             case 2: hipLaunchKernelGGL((k_splitk_reduce<T, 2>), dim3(blocks), dim3(256), 0, st, g); break;

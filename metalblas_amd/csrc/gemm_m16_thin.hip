@@ -1,0 +1,209 @@
+// Thin products on the matrix cores, bf16_t / f16_t: a handful of vectors (<= 16) against a
+// large matrix that is streamed from HBM exactly once.
+//
+//   * k_thin16 (mfma16.hpp), tile 32 x 256: the vectors are the rows of A (K-contiguous), the
+//     matrix B is N-contiguous; B goes through a 4-deep LDS-direct ring (512-byte row spans).
+//   * k_thin_dot (below), tile 64 x 16: the matrix A is K-contiguous and the vectors are the
+//     columns of B (K-contiguous).  The matrix never touches LDS: each wave loads 1 KiB of
+//     each of its 16 rows per 512-deep macro step straight into the registers that feed
+//     v_mfma_f32_16x16x32 (the row-contiguous stream of the GEMV kernels), double-buffered
+//     across macro steps.  Only the 16 x 512 vector
+//     slice of a step is staged in LDS, shared by the workgroup's 4 waves.
+//
+// The planner transposes the other two layout combinations into these two.
+#include "mfma16.hpp"
+
+namespace mb {
+namespace m16 {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <class T> __device__ __forceinline__ f32x4 mma16x16(uint4 a, uint4 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mma16x16<bf16_t>(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mma16x16<f16_t>(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+}
+
+// 16-byte buffer load; offsets past the resource's 2 GiB range read zeros (the
+// offsets used below stay under 2^32)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+// C (M x N, N <= 16) = A (M x K, K-contiguous) @ B (K x N, K-contiguous), fp32 accumulation.
+// Workgroup: 4 waves x 16 rows of A; grid (ceil(M / 64), K slices, batch).  g.k_chunk is a
+// multiple of KS and K a multiple of 8, so a 16-byte chunk is either inside the slice or past
+// its end (then it contributes zeros).
+//
+// v_mfma_f32_16x16x32 takes, in lane l, 8 consecutive k of row l % 16 of its first operand and
+// of column l % 16 of its second, for the k group l / 16, and returns D[4 (l / 16) + i][l % 16].
+// MFMA j of a step covers k0 + 32 j .. k0 + 32 j + 31.  The first operand is the vector slice (rows n), the second the matrix rows
+// (columns m): lane l ends with C[m0 + l % 16][4 (l / 16) + i].
+template <class T>
+__global__ __launch_bounds__(256) void k_thin_dot(GemmArgs g) {
+    constexpr int KS = 512, XP = KS + 8;   // k per macro step; LDS row pitch (conflict-free reads)
+    __shared__ __attribute__((aligned(16))) T xs[2][16][XP];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: the resource stays scalar
+    const int r = lane & 15, grp = lane >> 4;
+    const int m0 = blockIdx.x * 64 + 16 * w;
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.k_chunk;
+    const int kend = min(g.K, kbeg + g.k_chunk);
+    const int nsteps = cdiv(kend - kbeg, KS);
+    // rows past M repeat row M - 1: their values are never stored
+    const int mbase = min(m0, g.M - 1), mrow = min(m0 + r, g.M - 1);
+    // byte offset of this lane's row and k group from the wave's first row (the host checks
+    // 16 rows + K fit in 31 bits)
+    const uint32_t lane_off = (uint32_t)(((int64_t)(mrow - mbase) * g.a_rs + 8 * grp) * sizeof(T));
+    uint32_t x_off[4];   // byte offsets of this thread's vector chunks (k from the step start)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = tid + 256 * i;
+        x_off[i] = (uint32_t)(((int64_t)(c >> 6) * g.b_cs + 8 * (c & 63)) * sizeof(T));
+    }
+
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc((const T *)g.a + bz * g.a_bs + (int64_t)mbase * g.a_rs);
+        // vector n, K-contiguous: element k at (n * b_cs + k) from the batch's B
+        const __amdgpu_buffer_rsrc_t rb = buf_rsrc((const T *)g.b + bz * g.b_bs);
+
+        // this lane's 16 chunks of step st: k = kbeg + st KS + 32 j + 8 grp, so load j reads 64
+        // contiguous bytes of each of the wave's 16 rows and the wave's 16 loads cover 1 KiB
+        // of every row back to back (the chunk offset rides in the scalar offset: one VGPR
+        // addresses all 16 loads)
+        auto load_w = [&](int st, uint4 (&dst)[16]) {
+            const int kb = kbeg + st * KS;
+            if (kb + KS <= kend) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) dst[j] = ld_buf(ra, lane_off, kb * (int)sizeof(T) + 64 * j);
+            } else {   // the slice end: chunks past it load from an out-of-range offset (zeros)
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    dst[j] = ld_buf(ra, kb + 32 * j + 8 * grp < kend ? lane_off : 0x80000000u, kb * (int)sizeof(T) + 64 * j);
+            }
+        };
+        // the step's 16 x 512 vector slice: thread t moves chunks t + 256 i (vector c / 64,
+        // k chunk c % 64); vectors past N and k past the slice load from an out-of-range
+        // offset (zeros)
+        auto load_x = [&](int st, uint4 (&dst)[4]) {
+            const int kb = kbeg + st * KS;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = tid + 256 * i, n = c >> 6, kc = 8 * (c & 63);
+                const uint32_t off = n < g.N && kb + kc < kend ? x_off[i] : 0x80000000u;
+                dst[i] = ld_buf(rb, off, kb * (int)sizeof(T));
+            }
+        };
+        auto store_x = [&](int buf, const uint4 (&src)[4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int c = tid + 256 * i;
+                *(uint4 *)&xs[buf][c >> 6][8 * (c & 63)] = src[i];
+            }
+        };
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        // vector fragments are read two MFMAs ahead (not all 16 up front: registers)
+        auto compute = [&](const uint4 (&wr)[16], int buf) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint4 xf = *(const uint4 *)&xs[buf][r][32 * j + 8 * grp];
+                acc = mma16x16<T>(xf, wr[j], acc);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int j = 0; j < 14; ++j) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        };
+
+        // matrix chunks one step ahead (wa / wb), vector slices two steps ahead (xa / xb), so
+        // every wait is for loads issued a whole step earlier
+        uint4 wa[16], wb[16], xa[4], xb[4];
+        if (nsteps > 0) {
+            load_x(0, xa);
+            if (nsteps > 1) load_x(1, xb);
+            load_w(0, wa);
+            store_x(0, xa);
+            __syncthreads();
+        }
+        for (int st = 0; st < nsteps; st += 2) {
+            // step st: matrix chunks in wa, vectors in xs[0]
+            const bool more1 = st + 1 < nsteps;
+            if (more1) load_w(st + 1, wb);
+            if (st + 2 < nsteps) load_x(st + 2, xa);
+            compute(wa, 0);
+            if (more1) store_x(1, xb);
+            __syncthreads();   // xs[1] written; every wave is done with xs[0]
+            if (!more1) break;
+            // step st + 1: matrix chunks in wb, vectors in xs[1]
+            const bool more2 = st + 2 < nsteps;
+            if (more2) load_w(st + 2, wa);
+            if (st + 3 < nsteps) load_x(st + 3, xb);
+            compute(wb, 1);
+            if (more2) store_x(0, xa);
+            __syncthreads();
+        }
+
+        const int m = m0 + r;
+        if (m < g.M) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int n = 4 * grp + i;
+                if (n >= g.N) continue;
+                if (g.splits > 1) {
+                    float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
+                    ws[(int64_t)m * g.N + n] = acc[i];
+                } else {
+                    T *c = (T *)g.c + bz * g.c_bs + m * g.c_rs + n * g.c_cs;
+                    store_out<T>(g, c, acc[i], bz * g.bias_bs + m * g.bias_rs + n * g.bias_cs);
+                }
+            }
+        }
+        __syncthreads();   // xs reuse by the next batch iteration
+    }
+}
+
+}  // namespace
+
+// k_thin_dot addresses 16 rows of A (16 vectors of B) plus a K slice from one buffer
+// resource: 31-bit offsets
+bool thin_dot_offsets_fit(const GemmArgs &g) {
+    const int64_t lim = (int64_t)1 << 31;
+    return (16 * g.a_rs + g.K + 512) * 2 < lim && (16 * g.b_cs + g.K + 512) * 2 < lim;
+}
+
+hipError_t launch_thin(int dt, bool ktail, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid,
+                       hipStream_t st) {
+    if (t.bm == 64 && t.bn == 16) {
+        if (!a_kc || !b_kc || g.N > 16 || (g.K & 7) || (g.k_chunk & 511) || !thin_dot_offsets_fit(g))
+            return hipErrorInvalidValue;
+        dim3 grid2(cdiv(g.M, 64), g.splits, grid.z);
+        if (dt == BF16) hipLaunchKernelGGL((k_thin_dot<bf16_t>), grid2, dim3(256), 0, st, g);
+        else if (dt == F16) hipLaunchKernelGGL((k_thin_dot<f16_t>), grid2, dim3(256), 0, st, g);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
+    if (dt == BF16)
+        return ktail ? launch_thin16<bf16_t, true>(t, a_kc, b_kc, g, grid, st)
+                     : launch_thin16<bf16_t, false>(t, a_kc, b_kc, g, grid, st);
+    if (dt == F16)
+        return ktail ? launch_thin16<f16_t, true>(t, a_kc, b_kc, g, grid, st)
+                     : launch_thin16<f16_t, false>(t, a_kc, b_kc, g, grid, st);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace m16
+}  // namespace mb

@@ -22,6 +22,7 @@ hipError_t launch_f16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStre
 hipError_t launch_i8_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_thin(int dt, bool ktail, const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 }  // namespace m16
 
 namespace {
@@ -38,6 +39,9 @@ constexpr TileEntry kTiles[] = {
 constexpr TileEntry kTiles16[] = {
     {256, 256, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
     {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
+    // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 (A and B
+    // K-contiguous), k_thin16 32 x 256 (A K-contiguous, B N-contiguous)
+    {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},
 };
 
 // dtypes of the LDS-direct family
@@ -92,6 +96,8 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
         const int es = dtype_size(dt), bk = 128 / es;
         if (m16_offsets_fit(t, a_kc, b_kc, g, es)) {
             const bool whole = (g.k_chunk % bk) == 0 && (g.K % bk) == 0;
+            if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256))
+                return m16::launch_thin(dt, !whole, t, a_kc, b_kc, g, grid, st);
             if (t.sched == 1) {
                 if (dt == BF16) return m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st);
                 if (dt == F16) return m16::launch_f16_pp(!whole, a_kc, b_kc, g, grid, st);

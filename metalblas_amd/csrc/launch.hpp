@@ -112,6 +112,10 @@ hipError_t launch_pack(const PackArgs &a, hipStream_t st);
 hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st);
+namespace m16 {
+// whether k_thin_dot can address 16 rows of A plus a K slice with 31-bit buffer offsets
+bool thin_dot_offsets_fit(const GemmArgs &g);
+}  // namespace m16
 
 // gemv.hip
 int gemv_nv_bucket(int nv);   // template NV used for a given number of vectors
@@ -123,6 +127,9 @@ int gemv_axpy_vec(int dt, int nv);   // elements per lane of the vector path
 // the 16-byte vector width)
 bool gemv_fast_dtype(int dt);
 int gemv_fast_vec(int dt);
+// columns one workgroup of the fast axpy kernel covers when it uses column bands (nv == 1),
+// else 0
+int gemv_axpy_band_cols(int dt, int nv);
 hipError_t launch_gemv_dot_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_gemv_axpy_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 

@@ -268,7 +268,12 @@ bool plan_gemv(const Prob &p, Plan &pl) {
         const int vv = ok ? V : 1;
         const int64_t waves = ((int64_t)g.rows + 64 * vv - 1) / (64 * vv) * p.batch;
         const int cus = dev_info().cus;
-        int64_t splits = (8LL * cus + waves - 1) / waves;
+        int64_t splits = (8LL * cus + waves - 1) / waves;   // about 8 waves per CU
+        const int band = fast ? gemv_axpy_band_cols(p.dt, (int)nv) : 0;
+        if (band > 0) {   // column-band kernel: one 4-wave workgroup per CU
+            const int64_t blocks = ((int64_t)g.rows + band - 1) / band * p.batch;
+            splits = (cus + blocks - 1) / blocks;
+        }
         const int64_t max_splits = (p.K + 63) / 64;
         if (splits > max_splits) splits = max_splits;
         if (splits > 256) splits = 256;
@@ -294,7 +299,10 @@ bool plan_gemv(const Prob &p, Plan &pl) {
 // an explicit wave grid (WM, WN) and schedule are honoured when compiled; BK is fixed by the
 // dtype.  The reference's (BM, BN, NSG) form for backend="mpp_tensor" leaves WM/WN at 0 and
 // gets the default 2 x 2 wave grid.
-MfmaTile snap_tile(int dt, const int32_t *t) {
+// the thin-product tiles (k_thin_dot 64 x 16, k_thin16 32 x 256)
+bool thin_tile(const MfmaTile &t) { return (t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256); }
+
+MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc) {
     MfmaTile want = {t[0], t[1], 2, 2};
     if (t[3] > 0 && t[4] > 0) {
         want.wm = t[3];
@@ -306,6 +314,11 @@ MfmaTile snap_tile(int dt, const int32_t *t) {
     int best = 0;
     double bestd = 1e30;
     for (int i = 0; i < n && i < 32; ++i) {
+        // thin tiles: bf16 / fp16, 64 x 16 with both operands K-contiguous, 32 x 256 with A
+        // K-contiguous and B N-contiguous
+        if (thin_tile(list[i]) && ((dt != MB_DTYPE_BF16 && dt != MB_DTYPE_F16) ||
+                                   (list[i].bm == 64 ? !(a_kc && b_kc) : !(a_kc && !b_kc))))
+            continue;
         double d = fabs(log2((double)list[i].bm / (want.bm > 0 ? want.bm : 1))) +
                    fabs(log2((double)list[i].bn / (want.bn > 0 ? want.bn : 1)));
         if (list[i].wm != want.wm || list[i].wn != want.wn) d += 0.01;
@@ -351,7 +364,8 @@ bool mfma_layout_ok(const Prob &p, bool &a_kc, bool &b_kc) {
 // of 16 bytes).  The copy keeps the operand's orientation (K-contiguous if it has no unit
 // stride) and zero-pads the contiguous extent; when K is padded every K-contiguous operand
 // is copied so that the padding contributes zeros.  Returns the workspace bytes used.
-int64_t plan_packs(Prob &p, Plan &pl) {
+// Bit w of force_kc (0 = A, 1 = B) asks for that operand K-contiguous whatever its layout.
+int64_t plan_packs(Prob &p, Plan &pl, int force_kc = 0) {
     const int es = dtype_size(p.dt), E = 16 / es;
     int64_t ws = 0;
     const char *placeholder = (const char *)(uintptr_t)4096;   // aligned stand-in until run time
@@ -360,7 +374,8 @@ int64_t plan_packs(Prob &p, Plan &pl) {
         Operand &o = is_a ? p.a : p.b;
         int orient = is_a ? a_orient(p) : b_orient(p);
         bool need = !operand_ok(o, orient, is_a, p);
-        if (orient < 0) orient = 1;
+        if (((force_kc >> which) & 1) && orient != 1) need = true;
+        if (orient < 0 || ((force_kc >> which) & 1)) orient = 1;
         if (orient == 1 && p.K % E) need = true;
         if (!need) continue;
         PackOp &pk = pl.pack[which];
@@ -397,7 +412,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     // the autotuner puts the tile it measured fastest)
     const bool forced = p.tile[0] > 0 && p.tile[1] > 0;
     if (forced) {
-        t = snap_tile(p.dt, p.tile);
+        t = snap_tile(p.dt, p.tile, a_kc, b_kc);
     } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8) {
         // Occupancy-aware cost model over the LDS-direct 16-bit tiles.  occ = workgroups per
         // CU (LDS and VGPR limited), eff = relative per-CU throughput at that occupancy,
@@ -622,6 +637,70 @@ bool plan_complex(const Prob &p, Plan &pl) {
     return true;
 }
 
+// Products with a few vectors (2..16) and a large matrix run on the matrix cores, which read
+// the matrix once at HBM speed whatever the vector count (the VALU GEMV kernels spend nv FMAs
+// per matrix element, which outgrows the HBM stream from about 4 vectors up).  Two thin tiles:
+//   64 x 16  (k_thin_dot): matrix = A, K-contiguous; vectors = columns of B;
+//   32 x 256 (k_thin16):   matrix = B, N-contiguous; vectors = rows of A.
+// The other two layouts are the transposed problem of these.  The vectors must be
+// K-contiguous and are copied (nv x K elements) when they are not; a matrix the loaders cannot
+// stream in place is left to the GEMV path.  K is split so that one workgroup runs per CU.
+// bf16 / fp16 only.
+// Measured on MI355X (bf16, 16384^2 matrix): the 32 x 256 tile streams at ~92 us for every
+// vector count from 2 up (VALU: 95 us at 2 vectors, 118 at 8, 189 at 16); the 64 x 16 tile at
+// ~120 us (VALU: 95-97 us up to 4 vectors, 195 at 8, 624 at 16).
+constexpr int kThinMfmaMinNvRows = 2, kThinMfmaMinNvDot = 5;
+
+bool plan_thin_mfma(const Prob &p, Plan &pl) {
+    if (p.dt != MB_DTYPE_BF16 && p.dt != MB_DTYPE_F16) return false;
+    if (p.tile[0] > 0 && p.tile[1] > 0) {   // an explicit tile: only a thin one keeps this plan
+        const MfmaTile req = {p.tile[0], p.tile[1], 0, 0, 0};
+        if (!thin_tile(req)) return false;
+    }
+    const bool vec_b = p.N <= p.M;   // vectors are the columns of B
+    const int64_t nv = vec_b ? p.N : p.M, wide = vec_b ? p.M : p.N;
+    if (nv > 16 || wide < 2048 || p.K < 2048) return false;
+    const int mo = vec_b ? a_orient(p) : b_orient(p);   // the matrix: 1 = K-contiguous
+    if (mo < 0 || nv < (mo == 1 ? kThinMfmaMinNvDot : kThinMfmaMinNvRows)) return false;
+    Prob q = p;
+    if ((mo == 1) != vec_b) transpose(q);   // K-contiguous matrix as A, N-contiguous as B
+    const bool dot = mo == 1;
+    Plan trial;
+    const int64_t pack_bytes = plan_packs(q, trial, dot ? 2 : 1);   // vectors K-contiguous
+    if (trial.pack[dot ? 0 : 1].on) return false;                    // never copy the matrix
+    bool a_kc = false, b_kc = false;
+    if (!mfma_layout_ok(q, a_kc, b_kc) || !(dot ? a_kc && b_kc : a_kc && !b_kc)) return false;
+    const MfmaTile t = dot ? MfmaTile{64, 16, 4, 1, 0} : MfmaTile{32, 256, 1, 4, 0};
+    q.tile[0] = t.bm; q.tile[1] = t.bn; q.tile[2] = 0; q.tile[3] = t.wm; q.tile[4] = t.wn; q.tile[5] = t.sched + 1;
+    const int64_t req_split = q.split_req;
+    q.split_req = 1;
+    pl.pack[0] = trial.pack[0];
+    pl.pack[1] = trial.pack[1];
+    pl.p = q;
+    plan_mfma(q, pl, a_kc, b_kc);
+    if (pl.tile.bm != t.bm || pl.tile.bn != t.bn) return false;
+    if (dot && !m16::thin_dot_offsets_fit(pl.gg)) return false;
+    // K slices: whole macro steps (512) for k_thin_dot, whole stages for k_thin16, at least
+    // two / four of them per slice
+    const int64_t unit = dot ? 512 : 128 / dtype_size(q.dt);
+    const int64_t tiles = (dot ? (q.M + 63) / 64 : (q.N + 255) / 256) * q.batch, cus = dev_info().cus;
+    int64_t splits = req_split > 0 ? req_split : (cus + tiles - 1) / tiles;
+    const int64_t maxs = q.K / ((dot ? 2 : 4) * unit);
+    if (req_split <= 0 && splits > maxs) splits = maxs;
+    if (splits > 64) splits = 64;
+    if (splits < 1) splits = 1;
+    int64_t chunk = (q.K + splits - 1) / splits;
+    chunk = (chunk + unit - 1) / unit * unit;
+    splits = (q.K + chunk - 1) / chunk;
+    GemmArgs &g = pl.gg;
+    g.splits = (int)splits;
+    g.k_chunk = (int)(splits > 1 ? chunk : (dot ? (q.K + 511) / 512 * 512 : q.K));
+    pl.ws_bytes = splits > 1 ? splits * q.batch * q.M * q.N * acc_size(q.dt) : 0;
+    pl.split_off = pack_bytes;
+    pl.ws_bytes += pack_bytes;
+    return true;
+}
+
 // allow_ws = false plans without any workspace use: no operand copies and no split-K.
 int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
     Prob p;
@@ -649,6 +728,13 @@ int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
         return MB_OK;
     }
     const bool thin = p.M <= 16 || p.N <= 16;
+    if (p.backend == MB_BACKEND_AUTO && thin && allow_ws) {
+        Plan tp = pl;
+        if (plan_thin_mfma(p, tp)) {
+            pl = tp;
+            return MB_OK;
+        }
+    }
     if (p.backend == MB_BACKEND_GEMV || (p.backend == MB_BACKEND_AUTO && thin)) {
         if (plan_gemv(p, pl)) {
             if (!allow_ws) drop_splits(pl);
@@ -851,12 +937,13 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
         ++out;
     };
     emit(pl.tile);
+    if (thin_tile(pl.tile)) return 1;   // thin products have one matrix-core tile
     for (int i = 0; i < n && i < 32; ++i) {
         const MfmaTile &t = list[i];
         if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn &&
             t.sched == pl.tile.sched)
             continue;
-        if (t.bm > 2 * pl.p.M + 32 || t.bn > 2 * pl.p.N + 32) continue;
+        if (t.bm > 2 * pl.p.M + 32 || t.bn > 2 * pl.p.N + 32 || thin_tile(t)) continue;
         emit(t);
     }
     return out < cap ? out : cap;

@@ -512,6 +512,134 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     }
 }
 
+// Thin products (a handful of vectors against a large matrix): the 32-wide operand tile is
+// shared by every workgroup and stays in L2, the wide one is streamed from HBM exactly once.
+// Instead of k_gemm16's two LDS buffers plus L2 prefetch (whose lines, at 64 workgroups per
+// XCD, are evicted from the 4 MiB L2 before use), NST LDS buffers are in flight: the loads of
+// stage kt + NST - 1 are issued right after the barrier that publishes stage kt, so each
+// workgroup keeps (NST - 1) x 32 KiB of the wide operand on the way.  The matrix cores do
+// 2 MFMAs per 16-deep k-step per wave; they are not the limit.
+template <int N> __device__ __forceinline__ void vm_wait_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL, int NST>
+__global__ __launch_bounds__(64 * WM * WN) void k_thin16(GemmArgs g) {
+    constexpr int NW = WM * WN;
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int ES = sizeof(T);
+    constexpr int BK = 128 / ES;
+    using TA = Tile16<BM, NW, A_KC, ES>;
+    using TB = Tile16<BN, NW, B_KC, ES>;
+    constexpr int STAGE = TA::BYTES + TB::BYTES;
+    static_assert(TM >= 1 && TN >= 1 && NST >= 3, "thin tile");
+    static_assert(TA::SEGS % NW == 0 && TB::SEGS % NW == 0, "every wave issues the same loads");
+    constexpr int LPS = TA::PER_WAVE + TB::PER_WAVE;   // LDS-direct loads per stage and wave
+    static_assert((NST - 2) * LPS < 64, "vmcnt range");
+
+    __shared__ __attribute__((aligned(1024))) char smem[NST * STAGE];
+    const uint32_t smem_lds = lds_addr(smem);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave % WM, wn = wave / WM;
+    const int tiles_m = cdiv(g.M, BM), tiles_n = cdiv(g.N, BN);
+    int tm, tn;
+    tile_coords16(blockIdx.x, tiles_m, tiles_n, g.swz, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.k_chunk;
+    const int kend = min(g.K, kbeg + g.k_chunk);
+    const int klen = kend - kbeg;
+    const int nk = cdiv(klen, BK);
+    const int nfull = klen / BK;
+    const int64_t lda = A_KC ? g.a_rs : g.a_cs;
+    const int64_t ldb = B_KC ? g.b_cs : g.b_rs;
+    const int rows_a = g.M - m0, rows_b = g.N - n0;
+    const int stepa = (int)((A_KC ? (int64_t)BK : (int64_t)BK * lda) * ES);
+    const int stepb = (int)((B_KC ? (int64_t)BK : (int64_t)BK * ldb) * ES);
+
+    uint32_t offa[TA::PER_WAVE], offb[TB::PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < TA::PER_WAVE; ++i) offa[i] = TA::src_offset(wave + i * NW, lane, lda, rows_a, BK);
+#pragma unroll
+    for (int i = 0; i < TB::PER_WAVE; ++i) offb[i] = TB::src_offset(wave + i * NW, lane, ldb, rows_b, BK);
+    int fba[A_KC ? 1 : TM], fbb[B_KC ? 1 : TN];
+#pragma unroll
+    for (int j = 0; j < (A_KC ? 1 : TM); ++j) fba[j] = TA::frag_base(wm * WTM, lane, j);
+#pragma unroll
+    for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
+
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
+        const T *Ab = (const T *)g.a + bz * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
+        const T *Bb = (const T *)g.b + bz * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
+        const i32x4 ra = make_rsrc(Ab), rb = make_rsrc(Bb);
+
+        auto load_stage = [&](int kt) {
+            const uint32_t base = smem_lds + (kt % NST) * STAGE;
+            if (!KTAIL || kt < nfull) {
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i) dma16(ra, base + (wave + i * NW) * 1024, offa[i], kt * stepa);
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i)
+                    dma16(rb, base + TA::BYTES + (wave + i * NW) * 1024, offb[i], kt * stepb);
+            } else {
+                const int kleft = klen - kt * BK;
+#pragma unroll
+                for (int i = 0; i < TA::PER_WAVE; ++i)
+                    dma16(ra, base + (wave + i * NW) * 1024, TA::src_offset(wave + i * NW, lane, lda, rows_a, kleft),
+                          kt * stepa);
+#pragma unroll
+                for (int i = 0; i < TB::PER_WAVE; ++i)
+                    dma16(rb, base + TA::BYTES + (wave + i * NW) * 1024,
+                          TB::src_offset(wave + i * NW, lane, ldb, rows_b, kleft), kt * stepb);
+            }
+        };
+
+        typename AccV<T>::type acc[TN][TM];
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+#pragma unroll
+        for (int s = 0; s < NST - 1; ++s)
+            if (s < nk) load_stage(s);
+        for (int kt = 0; kt < nk; ++kt) {
+            // stage kt has landed once at most the loads of stages kt+1 .. kt+NST-2 are pending
+            if (kt + NST - 2 < nk) vm_wait_n<(NST - 2) * LPS>();
+            else vm_wait_all();
+            __syncthreads();   // stage kt visible to all waves; stage kt-1's buffer is free
+            if (kt + NST - 1 < nk) load_stage(kt + NST - 1);
+            const char *cur = smem + (kt % NST) * STAGE;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                uint4 fa[TM], fb[TN];
+#pragma unroll
+                for (int j = 0; j < TM; ++j) fa[j] = TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
+#pragma unroll
+                for (int i = 0; i < TN; ++i) fb[i] = TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[i], fa[j]);
+            }
+        }
+        store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        __syncthreads();   // LDS reuse by the next batch iteration
+    }
+}
+
+// The thin tile 32 x 256: the vectors are the rows of A (K-contiguous), the matrix B is
+// N-contiguous.  4 buffers of 36 KiB: one workgroup per CU.
+template <class T, bool KTAIL>
+hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    if (!(t.bm == 32 && t.bn == 256 && t.wm == 1 && t.wn == 4 && a_kc && !b_kc)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_thin16<T, 32, 256, 1, 4, true, false, KTAIL, 4>), grid, dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
 // Ping-pong schedule of the 256 x 256 tile with 8 waves, two per SIMD (waves w and w + 4
 // share SIMD w % 4).  The waves form two groups, 0..3 and 4..7, that alternate between a
 // memory phase (all LDS fragment reads of one stage into registers, plus this wave's

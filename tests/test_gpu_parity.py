@@ -357,6 +357,55 @@ def test_thin_addmm(dev, dtype, shape):
     assert_parity(got, a, b, bias=bias, beta=0.5, alpha=2.0, tag=f"thin addmm {dtype} {shape}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("nv", [2, 3, 5, 8, 12, 16])
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+@pytest.mark.parametrize("side", ["N", "M"])
+def test_thin_matrix_cores(dev, dtype, nv, layout, side):
+    """Thin products with a large matrix run on the 64 x 16 (K-contiguous matrix, from 5
+    vectors) or 32 x 256 (N-contiguous matrix) matrix-core tiles, split-K, vectors copied
+    K-contiguous when they are not: wide side 2304 (a partial tile), K = 2088 (a partial
+    stage / macro step)."""
+    g = gen(300 + nv)
+    wide, K = 2304, 2088
+    if side == "N":
+        a = rand((wide, K), dtype, g) if layout[0] == "r" else rand((K, wide), dtype, g).t()
+        b = rand((K, nv), dtype, g) if layout[1] == "r" else rand((nv, K), dtype, g).t()
+    else:
+        a = rand((nv, K), dtype, g) if layout[0] == "r" else rand((K, nv), dtype, g).t()
+        b = rand((K, wide), dtype, g) if layout[1] == "r" else rand((wide, K), dtype, g).t()
+    ad, bd = _to(a, dev), _to(b, dev)
+    p = mb.kernels.plan(ad, bd)
+    dot = (side == "N" and layout[0] == "r") or (side == "M" and layout[1] == "c")   # K-contiguous matrix
+    if nv >= (5 if dot else 2):
+        assert p["family"] == "mfma" and p["tile"][:2] == ((64, 16) if dot else (32, 256)), p
+    got = mb.matmul(ad, bd)
+    assert_parity(got, a, b, tag=f"thin mfma {dtype} nv={nv} {layout} {side}")
+
+
+@pytest.mark.parametrize("case", ["bmm", "broadcast", "addmm", "kodd"])
+def test_thin_matrix_cores_more(dev, case):
+    """Batched and broadcast thin products, the fused epilogue, and an odd K (the matrix
+    cannot be streamed in place: the GEMV path takes it)."""
+    g = gen(11)
+    dt = torch.bfloat16
+    if case == "bmm":
+        a, b = rand((3, 2304, 2088), dt, g), rand((3, 2088, 8), dt, g)
+        assert_parity(mb.bmm(a.to(dev), b.to(dev)), a, b, tag="thin bmm")
+    elif case == "broadcast":
+        a, b = rand((3, 4, 2088), dt, g), rand((2088, 2304), dt, g)
+        got = mb.matmul(a.to(dev), b.to(dev))
+        assert_parity(got, a, b.expand(3, 2088, 2304), tag="thin broadcast")
+    elif case == "addmm":
+        a, b, bias = rand((2304, 2088), dt, g), rand((2088, 6), dt, g), rand((6,), dt, g)
+        got = mb.addmm(bias.to(dev), a.to(dev), b.to(dev), beta=0.5, alpha=-1.5)
+        assert_parity(got, a, b, bias=bias, beta=0.5, alpha=-1.5, tag="thin addmm mfma")
+    else:
+        a, b = rand((2304, 2051), dt, g), rand((2051, 8), dt, g)
+        assert mb.kernels.plan(a.to(dev), b.to(dev))["family"] != "mfma"
+        assert_parity(mb.matmul(a.to(dev), b.to(dev)), a, b, tag="thin odd K")
+
+
 @pytest.mark.parametrize("n", [8192, 16384])
 def test_gemv_config2_sizes(dev, n):
     """BASELINE config 2 at full size: y = W @ x, x @ W and 8-vector thin products,

@@ -164,10 +164,19 @@ def test_plan_config2_gemv_families():
     assert _lib.FAMILY_NAMES[p.family] == "gemv_axpy" and p.tile[2] == 1
     # x @ W streams W along its rows: split over K to fill 256 CUs, partials in the workspace
     assert p.split_k > 1 and p.workspace_bytes == p.split_k * n * 4
+    # 8 vectors: the thin matrix-core tiles, one workgroup per CU
     X8 = torch.empty(8, n, dtype=torch.bfloat16)
-    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, X8, W).family] == "gemv_axpy"
-    Xn = torch.empty(n, 8, dtype=torch.bfloat16)
-    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, W, Xn).family] == "gemv_dot"
+    p = _plan(torch.bfloat16, X8, W)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (32, 256)
+    assert p.split_k * (n // 256) == 256
+    Xn = torch.empty(n, 8, dtype=torch.bfloat16)   # N-contiguous vectors: copied K-contiguous
+    p = _plan(torch.bfloat16, W, Xn)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (64, 16) and p.split_k == 1
+    assert p.workspace_bytes == n * 8 * 2
+    # few vectors against a K-contiguous matrix stay on the VALU GEMV kernel
+    assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, W, torch.empty(n, 4, dtype=torch.bfloat16)).family] == "gemv_dot"
+    # fp32 stays on the VALU kernels
+    assert _lib.FAMILY_NAMES[_plan(torch.float32, torch.empty(8, n), torch.empty(n, n)).family] == "gemv_axpy"
 
 
 def test_plan_config4_splitk_and_batches():
