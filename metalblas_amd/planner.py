@@ -13,8 +13,11 @@ Restates the reference's autotuner (metalblas/float_dispatch.py:411-481: ``_prob
   * the winner is cached per (device, dtype, batch, M, N, K, layout, alignment) key; with
     ``METALBLAS_PLAN_CACHE=<file>`` the cache persists as JSON across processes.
 
-``METALBLAS_AUTOTUNE=0`` disables tuning (float_dispatch.py:156).  Timing uses HIP events on
-torch's current stream.
+Tuning is opt-in here: ``METALBLAS_AUTOTUNE=1`` enables it, anything else (or unset) keeps the
+C planner's static plans.  The reference tunes by default and reads ``METALBLAS_AUTOTUNE=0``
+as off (float_dispatch.py:156); this build turned the default off after a GPU memory fault,
+never reproduced or explained, during the one-shot tuning of a bf16 2048 x 4096 x 2048
+product on MI355X.  Timing uses HIP events on torch's current stream.
 """
 from __future__ import annotations
 
@@ -36,7 +39,7 @@ _loaded = False
 
 
 def enabled() -> bool:
-    return os.environ.get("METALBLAS_AUTOTUNE", "1") != "0"
+    return os.environ.get("METALBLAS_AUTOTUNE", "0") == "1"
 
 
 def probe_params(M, N, K):

@@ -312,6 +312,9 @@ def test_autotune_probe_params_and_cache(tmp_path, monkeypatch):
 
 
 def test_autotune_switch(monkeypatch):
+    """Opt-in: only METALBLAS_AUTOTUNE=1 enables the tuner."""
+    monkeypatch.delenv("METALBLAS_AUTOTUNE", raising=False)
+    assert not planner.enabled()
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "0")
     assert not planner.enabled()
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
