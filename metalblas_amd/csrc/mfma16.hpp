@@ -51,9 +51,17 @@ constexpr uint32_t kOOB = 0x80000000u;   // buffer offset that is always out of 
 // which exposes the whole global-load latency of the prefetched stage once per stage.  The
 // kernel instead waits for its own loads right before the barrier that publishes a stage,
 // when only that stage's loads (and one L2 prefetch) are in flight.  M0 carries the LDS
-// address; the s_nop covers the M0-write -> LDS-DMA hazard.
+// address.
+//
+// The compiler's hazard recognizer does not see the VMEM instruction inside the asm, so the
+// asm supplies its own wait states: on gfx950 a VMEM instruction that reads an SGPR written
+// by a VALU instruction needs 5 of them (the compiler emits `s_nop 4` for its own buffer
+// loads).  Such writes do occur right before these loads: SGPR spill reloads are
+// v_readlane_b32, and `readfirstlane` results.  With fewer wait states the load may read the
+// SGPR's previous value as its resource or offset, i.e. an arbitrary address.  `s_nop 4` also
+// covers the 1-wait-state M0 write -> LDS-DMA hazard.
 __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset, int soffset) {
-    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
                  : "memory");
@@ -63,9 +71,10 @@ __device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)
 __device__ __forceinline__ void vm_wait_but_one() { asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); }
 
 // L2 prefetch of one 128-byte line per lane: a dword LDS-direct load into a junk LDS area, so
-// no VGPR is written behind the compiler's back.  Out-of-range offsets load nothing.
+// no VGPR is written behind the compiler's back.  Out-of-range offsets load nothing.  Same
+// 5 wait states as dma16.
 __device__ __forceinline__ void pf_line(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset, int soffset) {
-    asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2 offen lds"
                  :
                  : "v"(voffset), "s"(rsrc), "s"(soffset), "{m0}"(lds_addr)
                  : "memory");
