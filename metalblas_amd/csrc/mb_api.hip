@@ -503,9 +503,11 @@ void plan_generic(const Prob &p, Plan &pl) {
     int64_t splits = 1;
     if (p.split_req > 1) {
         splits = p.split_req;
-    } else if (p.split_req == 0 && tiles < cus && p.K >= 1024) {
+    } else if (p.split_req == 0 && tiles < cus && p.K >= 128) {
+        // few output tiles: K slices of >= 16 (one LDS step) so that ~2 workgroups run per CU
+        // (int32 256^3: 16 tiles x 16 slices instead of 16 workgroups looping over K)
         splits = (2LL * cus + tiles - 1) / tiles;
-        const int64_t maxs = p.K / 256;
+        const int64_t maxs = p.K / 16;
         if (splits > maxs) splits = maxs;
         if (splits > 64) splits = 64;
         if (splits < 1) splits = 1;

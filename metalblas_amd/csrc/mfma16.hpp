@@ -767,12 +767,14 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             }
         };
         auto compute_stage = [&]() {
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s)
 #pragma unroll
                 for (int i = 0; i < TN; ++i)
 #pragma unroll
                     for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
+            __builtin_amdgcn_s_setprio(0);
         };
         auto phase_end = [&]() {
             __builtin_amdgcn_sched_barrier(0);
