@@ -180,6 +180,11 @@ void fill_gemm_args(const Prob &p, GemmArgs &g) {
     g.epilogue = p.epilogue; g.beta_nz = p.beta_nz; g.alpha_nz = p.alpha_nz;
     g.splits = 1;
     g.k_chunk = (int)(p.K > 0 ? p.K : 1);
+    {
+        const int es = dtype_size(p.dt);
+        g.bias_vec = !p.beta_nz || (p.bias.cs == 1 && p.bias.rs % 4 == 0 && p.bias.bs % 4 == 0 &&
+                                    aligned(p.bias.ptr, 4 * es));
+    }
     g.swz = 0;
     g.s = p.s;
 }

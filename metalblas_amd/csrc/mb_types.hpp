@@ -207,6 +207,7 @@ struct GemmArgs {
     int32_t vec_ok;      // GEMV families: vectorised loads allowed
     int32_t planes;      // write accumulator planes to ws even with one K slice (a later
                          // reduction kernel finishes the output)
+    int32_t bias_vec;    // bias rows read as 4-element vectors (contiguous, 4-element aligned)
     EpiScalars s;
 };
 

@@ -331,6 +331,45 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
                     }
                 }
             }
+    } else if (g.vec_ok && g.bias_vec && !Tr<T>::is_complex) {
+        // fused epilogue with 4-element vector bias loads and output stores (addmm's bias
+        // row broadcast or a full bias matrix, both contiguous along N)
+        const T *Bb = (const T *)g.bias + bz * g.bias_bs;
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+                const int gm = mw + j * 32 + mrow;
+                if (gm >= g.M) continue;
+                T *row = Cb + gm * g.c_rs;
+                const T *brow = Bb + gm * g.bias_rs;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int gn = nw + i * 32 + 8 * q + nsub;
+                    if (gn + 3 < g.N) {
+                        T bv[4], o[4];
+                        if (g.beta_nz) __builtin_memcpy(bv, brow + gn, 4 * sizeof(T));
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            o[r] = Tr<T>::down(epi_apply<T>((A)acc[i][j][4 * q + r], bv + r, g.s, g.beta_nz, g.alpha_nz));
+                        if constexpr (sizeof(T) == 2) {
+                            uint2 u;
+                            __builtin_memcpy(&u, o, 8);
+                            *(uint2 *)(row + gn) = u;
+                        } else {
+                            uint32_t u;
+                            __builtin_memcpy(&u, o, 4);
+                            *(uint32_t *)(row + gn) = u;
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (gn + r < g.N)
+                                store_out<T>(g, row + gn + r, (A)acc[i][j][4 * q + r],
+                                             bz * g.bias_bs + gm * g.bias_rs + gn + r);
+                    }
+                }
+            }
     } else {
 #pragma unroll
         for (int i = 0; i < TN; ++i)
