@@ -410,6 +410,20 @@ int64_t plan_packs(Prob &p, Plan &pl, int force_kc = 0) {
     return ws;
 }
 
+// K slices of a matrix-core plan with `tiles` output tiles: an explicit request, or under the
+// AUTO backend enough slices for ~2 workgroups per CU when the tiles alone leave CUs idle (K
+// slices of >= 4 stages, at most 64).
+int64_t auto_splits(const Prob &p, int64_t tiles, int bk) {
+    if (p.split_req > 1) return p.split_req;
+    const int cus = dev_info().cus;
+    if (p.split_req != 0 || p.backend != MB_BACKEND_AUTO || tiles >= cus || p.K < 2048) return 1;
+    int64_t s = (2LL * cus + tiles - 1) / tiles;
+    const int64_t maxs = p.K / (4 * bk);
+    if (s > maxs) s = maxs;
+    if (s > 64) s = 64;
+    return s < 1 ? 1 : s;
+}
+
 void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const int cus = dev_info().cus;
     MfmaTile t;
@@ -419,27 +433,34 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     if (forced) {
         t = snap_tile(p.dt, p.tile, a_kc, b_kc);
     } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8) {
-        // Occupancy-aware cost model over the LDS-direct 16-bit tiles.  occ = workgroups per
-        // CU (LDS and VGPR limited), eff = relative per-CU throughput at that occupancy,
-        // measured on a bf16 8192^3 product on MI355X.  Time ~ rounds * occ * BM*BN / eff.
+        // Cost model over the LDS-direct 16-bit tiles, in units of one CU's matrix-core time
+        // at the ping-pong kernel's rate (~4.8 TFLOP/s per CU, bf16): rounds x tiles resident
+        // per CU x BM*BN*K_slice / eff, plus the split-K reduction (partial planes written and
+        // read at ~5 TB/s, and a launch).  occ = workgroups per CU (LDS/VGPR limited); eff =
+        // relative per-CU throughput, measured on MI355X (bf16 8192^3, 4096^3, 2048^2 x 4096,
+        // 1024^2 x 8192, 4096 x 1024 x 4096).
         struct Cand {
             MfmaTile t;
             int occ;
             double eff;
         };
         static const Cand cands[] = {
-            {{256, 256, 2, 4, 1}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.91}, {{256, 128, 2, 2}, 1, 0.79},
-            {{128, 256, 2, 2}, 1, 0.73}, {{128, 128, 2, 2}, 1, 0.52}, {{128, 64, 2, 2}, 2, 0.62},
-            {{64, 128, 2, 2}, 2, 0.70},  {{64, 64, 2, 2}, 3, 0.59},
+            {{256, 256, 2, 4, 1}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.85}, {{256, 128, 2, 2}, 1, 0.79},
+            {{128, 256, 2, 2}, 1, 0.79}, {{128, 128, 2, 2}, 1, 0.70}, {{128, 64, 2, 2}, 2, 0.65},
+            {{64, 128, 2, 2}, 2, 0.60},  {{64, 64, 2, 2}, 3, 0.40},
         };
+        const int bk = 128 / dtype_size(p.dt);
         double best = 1e300;
         t = {64, 64, 2, 2};
         for (const auto &c : cands) {
             const int64_t tiles = ((p.M + c.t.bm - 1) / c.t.bm) * ((p.N + c.t.bn - 1) / c.t.bn) * p.batch;
-            const int64_t slots = (int64_t)cus * c.occ;
-            const int64_t rounds = (tiles + slots - 1) / slots;
-            const int64_t per_cu = tiles < cus ? 1 : (c.occ < (tiles + cus - 1) / cus ? c.occ : (tiles + cus - 1) / cus);
-            const double cost = (double)rounds * per_cu * c.t.bm * c.t.bn / c.eff;
+            const int64_t s = auto_splits(p, tiles, bk);
+            const int64_t wgs = tiles * s, slots = (int64_t)cus * c.occ;
+            const int64_t rounds = (wgs + slots - 1) / slots;
+            const int64_t per_cu = std::min<int64_t>(c.occ, (wgs + cus - 1) / cus);
+            const int64_t kc = (p.K + s - 1) / s;
+            double cost = (double)rounds * per_cu * c.t.bm * c.t.bn * (double)kc / c.eff;
+            if (s > 1) cost += (double)s * p.M * p.N * p.batch * 3.84 + 7.2e6;
             if (cost < best * 0.999) {
                 best = cost;
                 t = c.t;
@@ -468,16 +489,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const int es = dtype_size(p.dt);
     const int BK = 8 * (16 / es);
     const int64_t tiles = ((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * p.batch;
-    int64_t splits = 1;
-    if (p.split_req > 1) {
-        splits = p.split_req;
-    } else if (p.split_req == 0 && p.backend == MB_BACKEND_AUTO && tiles < cus && p.K >= 2048) {
-        splits = (2LL * cus + tiles - 1) / tiles;
-        const int64_t maxs = p.K / (4 * BK);
-        if (splits > maxs) splits = maxs;
-        if (splits > 64) splits = 64;
-        if (splits < 1) splits = 1;
-    }
+    int64_t splits = auto_splits(p, tiles, BK);
     if (splits > 1) {
         int64_t chunk = (p.K + splits - 1) / splits;
         chunk = (chunk + BK - 1) / BK * BK;
