@@ -176,6 +176,152 @@ __global__ __launch_bounds__(256) void k_thin_dot(GemmArgs g) {
     }
 }
 
+// ---- k_thin_dot4: the K-contiguous matrix read as 4-row x 1 KiB streams --------------------
+// A probe that only streams a 16384^2 bf16 matrix reached 0.81 of 8 TB/s when each CU keeps
+// ~8 rows in flight, 4 waves reading consecutive 1 KiB pieces of the same rows, each load
+// instruction covering 4 rows x 256 bytes; with 16 rows per wave (the 16 x 16 MFMA layout of
+// k_thin_dot) it reached 0.58.  v_mfma_f32_4x4x4bf16_1k runs 16 independent 4 x 4 x 4 blocks:
+// lane 4 b + i holds row i of block b's A and column i of its B, and receives D_b[0..3][i].
+// Here block b is a k chunk, so one 16-byte load per lane (row i, 8 k) covers 4 rows x 128 k,
+// the two 4-k halves feed two MFMAs, and the 16 blocks' partial sums are added across lanes
+// after each row quad.
+//
+// Workgroup: 4 waves on the same row quad; wave w takes k quarter w of the workgroup's K
+// slice (kq = k_chunk / 4 = 128 U) and keeps that quarter of the vectors in registers for
+// every row quad it visits (G groups of 4 vectors).  Row quads rq = blockIdx.x + gridDim.x t;
+// the 4 quarters' sums meet in LDS.  The host guarantees k_chunk = 512 U, K % 8 == 0, N <= 4G,
+// and 31-bit offsets for the whole matrix and vector block.
+typedef __bf16 bf16x4t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4t __attribute__((ext_vector_type(4)));
+
+template <class T> __device__ __forceinline__ f32x4 mma4x4(uint2 a, uint2 b, f32x4 c);
+template <> __device__ __forceinline__ f32x4 mma4x4<bf16_t>(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(bf16x4t, a), __builtin_bit_cast(bf16x4t, b), c,
+                                                  0, 0, 0);
+}
+template <> __device__ __forceinline__ f32x4 mma4x4<f16_t>(uint2 a, uint2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(f16x4t, a), __builtin_bit_cast(f16x4t, b), c, 0, 0, 0);
+}
+
+constexpr int kDot4U = 8;   // 16-byte loads per lane per row quad (k quarter = 1024)
+static_assert(kThinDot4Chunk == 512 * kDot4U, "K slice of k_thin_dot4");
+
+template <class T, int G>
+__global__ __launch_bounds__(256) void k_thin_dot4(GemmArgs g) {
+    constexpr int U = kDot4U;
+    __shared__ float red[2][4][G][4][4];   // [parity][wave][group][row][column]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 3, b = lane >> 2;   // row / column index in the block; block = k chunk
+    const int ks = blockIdx.y;
+    const int kbeg = ks * g.k_chunk;
+    const int kend = min(g.K, kbeg + g.k_chunk);
+    const int kq0 = kbeg + w * (g.k_chunk >> 2);    // this wave's k quarter
+    const bool full = kq0 + 128 * U <= kend;         // no chunk of the quarter is past the slice
+    const int nquads = cdiv(g.M, 4);
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
+        const __amdgpu_buffer_rsrc_t ra = buf_rsrc((const T *)g.a + bz * g.a_bs);
+        const __amdgpu_buffer_rsrc_t rb = buf_rsrc((const T *)g.b + bz * g.b_bs);
+        // this lane's vector chunks: vector 4 q + i, k = kq0 + 128 u + 8 b
+        uint4 xr[G][U];
+#pragma unroll
+        for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int n = 4 * q + i, k = kq0 + 128 * u + 8 * b;
+                const uint32_t off = n < g.N && k < kend ? (uint32_t)(((int64_t)n * g.b_cs + k) * sizeof(T)) : 0x80000000u;
+                xr[q][u] = ld_buf(rb, off, 0);
+            }
+        // matrix chunks of row quad rq: row 4 rq + i (clamped), k = kq0 + 128 u + 8 b
+        auto load_w = [&](int rq, uint4 (&dst)[U]) {
+            const int row = min(4 * rq + i, g.M - 1);
+            const uint32_t base = (uint32_t)(((int64_t)row * g.a_rs + kq0 + 8 * b) * sizeof(T));
+            if (full) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) dst[u] = ld_buf(ra, base, 256 * u * (int)(sizeof(T) / 2));
+            } else {
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    dst[u] = ld_buf(ra, kq0 + 128 * u + 8 * b < kend ? base : 0x80000000u, 256 * u * (int)(sizeof(T) / 2));
+            }
+        };
+        auto quad = [&](int rq, const uint4 (&wr)[U], int parity) {
+            f32x4 acc[G];
+#pragma unroll
+            for (int q = 0; q < G; ++q) acc[q] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int q = 0; q < G; ++q) {
+                    acc[q] = mma4x4<T>(make_uint2(wr[u].x, wr[u].y), make_uint2(xr[q][u].x, xr[q][u].y), acc[q]);
+                    acc[q] = mma4x4<T>(make_uint2(wr[u].z, wr[u].w), make_uint2(xr[q][u].z, xr[q][u].w), acc[q]);
+                }
+            // sum the 16 k-chunk blocks: lanes i, i + 4, ..., i + 60
+#pragma unroll
+            for (int q = 0; q < G; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = acc[q][r];
+                    v += __shfl_xor(v, 4, 64);
+                    v += __shfl_xor(v, 8, 64);
+                    v += __shfl_xor(v, 16, 64);
+                    v += __shfl_xor(v, 32, 64);
+                    acc[q][r] = v;
+                }
+            if (lane < 4) {
+#pragma unroll
+                for (int q = 0; q < G; ++q)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) red[parity][w][q][r][i] = acc[q][r];
+            }
+            __syncthreads();
+            // thread t < 16 G: group q = t / 16, row r = (t / 4) % 4, column c = t % 4
+            if (tid < 16 * G) {
+                const int q = tid >> 4, r = (tid >> 2) & 3, c = tid & 3;
+                const float v = red[parity][0][q][r][c] + red[parity][1][q][r][c] + red[parity][2][q][r][c] +
+                                red[parity][3][q][r][c];
+                const int m = 4 * rq + r, n = 4 * q + c;
+                if (m < g.M && n < g.N) {
+                    if (g.splits > 1) {
+                        float *ws = (float *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
+                        ws[(int64_t)m * g.N + n] = v;
+                    } else {
+                        T *cp = (T *)g.c + bz * g.c_bs + m * g.c_rs + n * g.c_cs;
+                        store_out<T>(g, cp, v, bz * g.bias_bs + m * g.bias_rs + n * g.bias_cs);
+                    }
+                }
+            }
+        };
+
+        // three row quads of matrix chunks in flight (wa, wb, wc rotate)
+        uint4 wa[U], wb[U], wc[U];
+        const int step = gridDim.x;
+        int rq = blockIdx.x;
+        if (rq < nquads) load_w(rq, wa);
+        if (rq + step < nquads) load_w(rq + step, wb);
+        int parity = 0;
+        while (rq < nquads) {
+            if (rq + 2 * step < nquads) load_w(rq + 2 * step, wc);
+            quad(rq, wa, parity);
+            parity ^= 1;
+            rq += step;
+            if (rq >= nquads) break;
+            if (rq + 2 * step < nquads) load_w(rq + 2 * step, wa);
+            quad(rq, wb, parity);
+            parity ^= 1;
+            rq += step;
+            if (rq >= nquads) break;
+            if (rq + 2 * step < nquads) load_w(rq + 2 * step, wb);
+            quad(rq, wc, parity);
+            parity ^= 1;
+            rq += step;
+        }
+        __syncthreads();   // red reuse by the next batch iteration
+    }
+}
+
 }  // namespace
 
 // k_thin_dot addresses 16 rows of A (16 vectors of B) plus a K slice from one buffer
@@ -185,8 +331,32 @@ bool thin_dot_offsets_fit(const GemmArgs &g) {
     return (16 * g.a_rs + g.K + 512) * 2 < lim && (16 * g.b_cs + g.K + 512) * 2 < lim;
 }
 
+bool thin_dot4_offsets_fit(const GemmArgs &g) {
+    const int64_t lim = (int64_t)1 << 31;
+    return ((int64_t)g.M * g.a_rs + g.K) * 2 < lim && ((int64_t)16 * g.b_cs + g.K) * 2 < lim;
+}
+
 hipError_t launch_thin(int dt, bool ktail, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid,
                        hipStream_t st) {
+    if (t.bm == 4 && t.bn == 16) {   // k_thin_dot4: grid (row-quad workgroups, K slices, batch)
+        if (!a_kc || !b_kc || g.N > 16 || (g.K & 7) || g.k_chunk != 512 * kDot4U || g.persist < 1 ||
+            !thin_dot4_offsets_fit(g))
+            return hipErrorInvalidValue;
+        dim3 grid2(g.persist, g.splits, grid.z);
+        const int G = (g.N + 3) / 4;
+#define MB_DOT4(GG) hipLaunchKernelGGL((k_thin_dot4<TT, GG>), grid2, dim3(256), 0, st, g)
+        if (dt == BF16) {
+            using TT = bf16_t;
+            if (G == 1) MB_DOT4(1); else if (G == 2) MB_DOT4(2); else if (G == 3) MB_DOT4(3); else MB_DOT4(4);
+        } else if (dt == F16) {
+            using TT = f16_t;
+            if (G == 1) MB_DOT4(1); else if (G == 2) MB_DOT4(2); else if (G == 3) MB_DOT4(3); else MB_DOT4(4);
+        } else {
+            return hipErrorInvalidValue;
+        }
+#undef MB_DOT4
+        return hipGetLastError();
+    }
     if (t.bm == 64 && t.bn == 16) {
         if (!a_kc || !b_kc || g.N > 16 || (g.K & 7) || (g.k_chunk & 511) || !thin_dot_offsets_fit(g))
             return hipErrorInvalidValue;

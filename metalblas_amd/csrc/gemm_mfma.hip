@@ -39,9 +39,10 @@ constexpr TileEntry kTiles[] = {
 constexpr TileEntry kTiles16[] = {
     {256, 256, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
     {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
-    // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 (A and B
-    // K-contiguous), k_thin16 32 x 256 (A K-contiguous, B N-contiguous)
-    {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},
+    // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 and
+    // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 (A K-contiguous, B
+    // N-contiguous)
+    {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},  {4, 16, 1, 1, 0},
 };
 
 // dtypes of the LDS-direct family
@@ -90,13 +91,13 @@ int mfma_list_tiles(int dt, MfmaTile *out, int cap) {
 hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, hipStream_t st,
                        LaunchShape *shape) {
     const int tiles = cdiv(g.M, t.bm) * cdiv(g.N, t.bn);
-    dim3 grid(tiles, g.splits, g.batch < 65535 ? g.batch : 65535);
-    if (shape) *shape = {grid, dim3(64 * t.wm * t.wn)};
+    dim3 grid(g.persist > 0 ? g.persist : tiles, g.splits, g.batch < 65535 ? g.batch : 65535);
+    if (shape) *shape = {grid, dim3(t.bm == 4 && t.bn == 16 ? 256 : 64 * t.wm * t.wn)};
     if (is16(dt) && !(t.bm == 32 && t.bn == 32)) {
         const int es = dtype_size(dt), bk = 128 / es;
         if (m16_offsets_fit(t, a_kc, b_kc, g, es)) {
             const bool whole = (g.k_chunk % bk) == 0 && (g.K % bk) == 0;
-            if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256))
+            if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256) || (t.bm == 4 && t.bn == 16))
                 return m16::launch_thin(dt, !whole, t, a_kc, b_kc, g, grid, st);
             if (t.sched == 1) {
                 if (dt == BF16) return m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st);

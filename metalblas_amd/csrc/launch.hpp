@@ -115,6 +115,9 @@ hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st);
 namespace m16 {
 // whether k_thin_dot can address 16 rows of A plus a K slice with 31-bit buffer offsets
 bool thin_dot_offsets_fit(const GemmArgs &g);
+// whether k_thin_dot4 can address the whole matrix and 16 vectors with 31-bit buffer offsets
+bool thin_dot4_offsets_fit(const GemmArgs &g);
+constexpr int kThinDot4Chunk = 4096;   // K per slice of k_thin_dot4 (4 waves x 8 loads x 128 k)
 }  // namespace m16
 
 // gemv.hip

@@ -305,7 +305,9 @@ bool plan_gemv(const Prob &p, Plan &pl) {
 // dtype.  The reference's (BM, BN, NSG) form for backend="mpp_tensor" leaves WM/WN at 0 and
 // gets the default 2 x 2 wave grid.
 // the thin-product tiles (k_thin_dot 64 x 16, k_thin16 32 x 256)
-bool thin_tile(const MfmaTile &t) { return (t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256); }
+bool thin_tile(const MfmaTile &t) {
+    return (t.bm == 64 && t.bn == 16) || (t.bm == 4 && t.bn == 16) || (t.bm == 32 && t.bn == 256);
+}
 
 MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc) {
     MfmaTile want = {t[0], t[1], 2, 2};
@@ -322,7 +324,7 @@ MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc) {
         // thin tiles: bf16 / fp16, 64 x 16 with both operands K-contiguous, 32 x 256 with A
         // K-contiguous and B N-contiguous
         if (thin_tile(list[i]) && ((dt != MB_DTYPE_BF16 && dt != MB_DTYPE_F16) ||
-                                   (list[i].bm == 64 ? !(a_kc && b_kc) : !(a_kc && !b_kc))))
+                                   (list[i].bn == 16 ? !(a_kc && b_kc) : !(a_kc && !b_kc))))
             continue;
         double d = fabs(log2((double)list[i].bm / (want.bm > 0 ? want.bm : 1))) +
                    fabs(log2((double)list[i].bn / (want.bn > 0 ? want.bn : 1)));
@@ -666,8 +668,8 @@ bool plan_complex(const Prob &p, Plan &pl) {
 // stream in place is left to the GEMV path.  K is split so that one workgroup runs per CU.
 // bf16 / fp16 only.
 // Measured on MI355X (bf16, 16384^2 matrix): the 32 x 256 tile streams at ~92 us for every
-// vector count from 2 up (VALU: 95 us at 2 vectors, 118 at 8, 189 at 16); the 64 x 16 tile at
-// ~120 us (VALU: 95-97 us up to 4 vectors, 195 at 8, 624 at 16).
+// vector count from 2 up (VALU: 95 us at 2 vectors, 118 at 8, 189 at 16); k_thin_dot4 at
+// ~111 us (VALU: 95-97 us at 2 and 4 vectors, 347 at 3, 195 at 8, 624 at 16).
 constexpr int kThinMfmaMinNvRows = 2, kThinMfmaMinNvDot = 5;
 
 bool plan_thin_mfma(const Prob &p, Plan &pl) {
@@ -680,7 +682,10 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     const int64_t nv = vec_b ? p.N : p.M, wide = vec_b ? p.M : p.N;
     if (nv > 16 || wide < 2048 || p.K < 2048) return false;
     const int mo = vec_b ? a_orient(p) : b_orient(p);   // the matrix: 1 = K-contiguous
-    if (mo < 0 || nv < (mo == 1 ? kThinMfmaMinNvDot : kThinMfmaMinNvRows)) return false;
+    if (mo < 0) return false;
+    // K-contiguous matrix: the VALU kernels stream 2 and 4 vectors faster (95-97 us vs
+    // ~111 us); 3 vectors have no fast VALU form (347 us)
+    if (mo == 1 ? (nv < kThinMfmaMinNvDot && nv != 3) : nv < kThinMfmaMinNvRows) return false;
     Prob q = p;
     if ((mo == 1) != vec_b) transpose(q);   // K-contiguous matrix as A, N-contiguous as B
     const bool dot = mo == 1;
@@ -689,7 +694,15 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     if (trial.pack[dot ? 0 : 1].on) return false;                    // never copy the matrix
     bool a_kc = false, b_kc = false;
     if (!mfma_layout_ok(q, a_kc, b_kc) || !(dot ? a_kc && b_kc : a_kc && !b_kc)) return false;
-    const MfmaTile t = dot ? MfmaTile{64, 16, 4, 1, 0} : MfmaTile{32, 256, 1, 4, 0};
+    // the K-contiguous matrix: k_thin_dot4 (4-row streams) when its 31-bit offsets cover the
+    // matrix, else k_thin_dot
+    bool dot4 = false;
+    if (dot) {
+        GemmArgs probe;
+        fill_gemm_args(q, probe);
+        dot4 = m16::thin_dot4_offsets_fit(probe);
+    }
+    const MfmaTile t = dot ? (dot4 ? MfmaTile{4, 16, 1, 1, 0} : MfmaTile{64, 16, 4, 1, 0}) : MfmaTile{32, 256, 1, 4, 0};
     q.tile[0] = t.bm; q.tile[1] = t.bn; q.tile[2] = 0; q.tile[3] = t.wm; q.tile[4] = t.wn; q.tile[5] = t.sched + 1;
     const int64_t req_split = q.split_req;
     q.split_req = 1;
@@ -701,19 +714,31 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     if (dot && !m16::thin_dot_offsets_fit(pl.gg)) return false;
     // K slices: whole macro steps (512) for k_thin_dot, whole stages for k_thin16, at least
     // two / four of them per slice
-    const int64_t unit = dot ? 512 : 128 / dtype_size(q.dt);
-    const int64_t tiles = (dot ? (q.M + 63) / 64 : (q.N + 255) / 256) * q.batch, cus = dev_info().cus;
-    int64_t splits = req_split > 0 ? req_split : (cus + tiles - 1) / tiles;
-    const int64_t maxs = q.K / ((dot ? 2 : 4) * unit);
-    if (req_split <= 0 && splits > maxs) splits = maxs;
-    if (splits > 64) splits = 64;
-    if (splits < 1) splits = 1;
-    int64_t chunk = (q.K + splits - 1) / splits;
-    chunk = (chunk + unit - 1) / unit * unit;
-    splits = (q.K + chunk - 1) / chunk;
+    const int64_t cus = dev_info().cus;
     GemmArgs &g = pl.gg;
+    int64_t splits;
+    if (dot4) {
+        // fixed K slices of m16::kThinDot4Chunk; a persistent grid of ~2 workgroups per CU that
+        // walks the row quads, so each workgroup loads its vector slice once
+        splits = (q.K + m16::kThinDot4Chunk - 1) / m16::kThinDot4Chunk;
+        g.k_chunk = m16::kThinDot4Chunk;
+        const int64_t quads = (q.M + 3) / 4;
+        int64_t wgs = (2 * cus + splits * q.batch - 1) / (splits * q.batch);
+        g.persist = (int)(wgs < quads ? wgs : quads);
+    } else {
+        const int64_t unit = dot ? 512 : 128 / dtype_size(q.dt);
+        const int64_t tiles = (dot ? (q.M + 63) / 64 : (q.N + 255) / 256) * q.batch;
+        splits = req_split > 0 ? req_split : (cus + tiles - 1) / tiles;
+        const int64_t maxs = q.K / ((dot ? 2 : 4) * unit);
+        if (req_split <= 0 && splits > maxs) splits = maxs;
+        if (splits > 64) splits = 64;
+        if (splits < 1) splits = 1;
+        int64_t chunk = (q.K + splits - 1) / splits;
+        chunk = (chunk + unit - 1) / unit * unit;
+        splits = (q.K + chunk - 1) / chunk;
+        g.k_chunk = (int)(splits > 1 ? chunk : (dot ? (q.K + 511) / 512 * 512 : q.K));
+    }
     g.splits = (int)splits;
-    g.k_chunk = (int)(splits > 1 ? chunk : (dot ? (q.K + 511) / 512 * 512 : q.K));
     pl.ws_bytes = splits > 1 ? splits * q.batch * q.M * q.N * acc_size(q.dt) : 0;
     pl.split_off = pack_bytes;
     pl.ws_bytes += pack_bytes;
@@ -918,8 +943,10 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
         info->tile[7] = pl.b_kc;
         info->split_k = pl.gg.splits;
         info->swizzle_log = pl.gg.swz;
-        info->block = 64 * pl.tile.wm * pl.tile.wn;
-        info->grid[0] = (int)(((pl.p.M + pl.tile.bm - 1) / pl.tile.bm) * ((pl.p.N + pl.tile.bn - 1) / pl.tile.bn));
+        const bool dot4 = pl.tile.bm == 4 && pl.tile.bn == 16;   // k_thin_dot4: 256 threads, persistent
+        info->block = dot4 ? 256 : 64 * pl.tile.wm * pl.tile.wn;
+        info->grid[0] = pl.gg.persist > 0 ? pl.gg.persist
+                                          : (int)(((pl.p.M + pl.tile.bm - 1) / pl.tile.bm) * ((pl.p.N + pl.tile.bn - 1) / pl.tile.bn));
         info->grid[1] = pl.gg.splits;
         info->grid[2] = (int)(pl.p.batch < 65535 ? pl.p.batch : 65535);
     } else if (pl.family == MB_FAMILY_GENERIC) {

@@ -208,6 +208,7 @@ struct GemmArgs {
     int32_t planes;      // write accumulator planes to ws even with one K slice (a later
                          // reduction kernel finishes the output)
     int32_t bias_vec;    // bias rows read as 4-element vectors (contiguous, 4-element aligned)
+    int32_t persist;     // workgroups of a persistent grid that loops over tiles (0: one per tile)
     EpiScalars s;
 };
 

@@ -362,10 +362,10 @@ def test_thin_addmm(dev, dtype, shape):
 @pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
 @pytest.mark.parametrize("side", ["N", "M"])
 def test_thin_matrix_cores(dev, dtype, nv, layout, side):
-    """Thin products with a large matrix run on the 64 x 16 (K-contiguous matrix, from 5
-    vectors) or 32 x 256 (N-contiguous matrix) matrix-core tiles, split-K, vectors copied
-    K-contiguous when they are not: wide side 2304 (a partial tile), K = 2088 (a partial
-    stage / macro step)."""
+    """Thin products with a large matrix run on the matrix cores: k_thin_dot4 (4 x 16,
+    K-contiguous matrix, from 5 vectors) or k_thin16 (32 x 256, N-contiguous matrix), split-K,
+    vectors copied K-contiguous when they are not: wide side 2304 (a partial tile), K = 2088
+    (a partial stage / K quarter)."""
     g = gen(300 + nv)
     wide, K = 2304, 2088
     if side == "N":
@@ -377,8 +377,8 @@ def test_thin_matrix_cores(dev, dtype, nv, layout, side):
     ad, bd = _to(a, dev), _to(b, dev)
     p = mb.kernels.plan(ad, bd)
     dot = (side == "N" and layout[0] == "r") or (side == "M" and layout[1] == "c")   # K-contiguous matrix
-    if nv >= (5 if dot else 2):
-        assert p["family"] == "mfma" and p["tile"][:2] == ((64, 16) if dot else (32, 256)), p
+    if (nv >= 5 or nv == 3) if dot else nv >= 2:
+        assert p["family"] == "mfma" and p["tile"][:2] == ((4, 16) if dot else (32, 256)), p
     got = mb.matmul(ad, bd)
     assert_parity(got, a, b, tag=f"thin mfma {dtype} nv={nv} {layout} {side}")
 

@@ -171,8 +171,8 @@ def test_plan_config2_gemv_families():
     assert p.split_k * (n // 256) == 256
     Xn = torch.empty(n, 8, dtype=torch.bfloat16)   # N-contiguous vectors: copied K-contiguous
     p = _plan(torch.bfloat16, W, Xn)
-    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (64, 16) and p.split_k == 1
-    assert p.workspace_bytes == n * 8 * 2
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (4, 16) and p.split_k == 4
+    assert p.workspace_bytes == n * 8 * 2 + 4 * n * 8 * 4   # the vector copy, then the K-slice planes
     # few vectors against a K-contiguous matrix stay on the VALU GEMV kernel
     assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, W, torch.empty(n, 4, dtype=torch.bfloat16)).family] == "gemv_dot"
     # fp32 stays on the VALU kernels
