@@ -242,7 +242,8 @@ def test_baddbmm_odd(dev, dtype, mnk):
 
 ND_CASES = [((64,), (64,)), ((32,), (32, 48)), ((40, 32), (32,)), ((32,), (8, 32, 48)),
             ((6, 40, 32), (32,)), ((8, 40, 32), (8, 32, 48)), ((8, 40, 32), (32, 48)),
-            ((40, 32), (8, 32, 48)), ((2, 3, 40, 32), (2, 3, 32, 48)), ((3, 1, 64, 32), (1, 5, 32, 48))]
+            ((40, 32), (8, 32, 48)), ((2, 3, 40, 32), (2, 3, 32, 48)), ((3, 1, 64, 32), (1, 5, 32, 48)),
+            ((2, 3, 40, 32), (32, 48))]
 
 
 def _torch_ref_nd(a, b):
@@ -253,6 +254,24 @@ def _torch_ref_nd(a, b):
     M, K = a2.shape[-2:]
     N = b2.shape[-1]
     return a2, b2, batch, M, N, K
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.int32], ids=str)
+@pytest.mark.parametrize("view", ["contiguous", "row_sliced", "batch_transposed"])
+def test_nd_fold_into_rows(dev, dtype, view):
+    """(..., M, K) @ (K, N): A's leading dims fold into its rows when that is a view (one 2-D
+    product), else the broadcast-batch path; both give the batched result."""
+    g = gen(5)
+    if view == "contiguous":
+        a = rand((4, 96, 64), dtype, g)
+    elif view == "row_sliced":
+        a = rand((4, 192, 64), dtype, g)[:, ::2]
+    else:
+        a = rand((96, 4, 64), dtype, g).transpose(0, 1)
+    b = rand((64, 80), dtype, g)
+    got = mb.matmul(_to(a, dev), b.to(dev))
+    assert got.shape == (4, 96, 80) and got.dtype == dtype
+    assert_parity(got, a, b.expand(4, 64, 80), tag=f"nd fold {dtype} {view}")
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16, torch.complex64,
