@@ -784,6 +784,27 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                               : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
             pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
         };
+        // load `op` of prefetch(kt), in the same order: the A segments, the B segments, then the
+        // L2-prefetch line (so the wait for "all but the most recent load" still works)
+        constexpr int NOPS = TA::PER_WAVE + TB::PER_WAVE + 1;
+        auto prefetch_op = [&](int kt, int op) {
+            const uint32_t base = smem_lds + (kt & 1) * STAGE;
+            const bool edge = KTAIL && kt >= nfull;
+            const int kleft = klen - kt * BK;
+            if (op < TA::PER_WAVE) {
+                const int seg = wave + op * NW;
+                dma16(ra, base + seg * 1024, edge ? TA::src_offset(seg, lane, lda, rows_a, kleft) : offa[op], kt * stepa);
+            } else if (op < TA::PER_WAVE + TB::PER_WAVE) {
+                const int ib = op - TA::PER_WAVE, seg = wave + ib * NW;
+                dma16(rb, base + TA::BYTES + seg * 1024, edge ? TB::src_offset(seg, lane, ldb, rows_b, kleft) : offb[ib],
+                      kt * stepb);
+            } else {
+                const int kp = kt + kPfDist;
+                const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
+                                  : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+                pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
+            }
+        };
 
         typename AccV<T>::type acc[TN][TM];
 #pragma unroll
@@ -815,6 +836,27 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
             __builtin_amdgcn_s_setprio(0);
         };
+        // the same MFMAs with prefetch(pk)'s loads issued one after each of the first NOPS
+        // MFMAs, so their issue (and the 5 wait states each carries) overlaps the matrix cores
+        // instead of delaying the first MFMA
+        auto compute_stage_pf = [&](bool do_pf, int pk) {
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+                        mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
+                        const int idx = (s * TN + i) * TM + j;
+                        if (idx < NOPS) {   // a uniform branch; one code path keeps the registers in check
+                            __builtin_amdgcn_sched_barrier(0);
+                            if (do_pf) prefetch_op(pk, idx);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+            __builtin_amdgcn_s_setprio(0);
+        };
         auto phase_end = [&]() {
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
@@ -841,8 +883,8 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     read_stage(kt);                 // phase 2kt+1
                     vm_wait_but_one();
                     phase_end();
-                    if (kt + 2 < nk) prefetch(kt + 2);   // phase 2kt+2
-                    compute_stage();
+                    compute_stage_pf(kt + 2 < nk, kt + 2);   // phase 2kt+2: prefetch(kt+2) inside
+
                     if (kt + 1 < nk) phase_end();
                 }
             }
