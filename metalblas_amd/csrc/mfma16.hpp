@@ -141,6 +141,30 @@ template <> __device__ __forceinline__ void mma16<int8_t>(i32x16 &c, uint4 a, ui
 }
 template <> __device__ __forceinline__ void mma16<uint8_t>(i32x16 &c, uint4 a, uint4 b) { mma16<int8_t>(c, a, b); }
 
+// 16 x 16 x 32 blocks (16-bit inputs only).  Per flop they draw markedly less power than the
+// 32 x 32 x 16 form: a probe that streams register-resident N(0,1) bf16 operands through each
+// shape runs the 16 x 16 x 32 one at ~2.0 GHz and the 32 x 32 x 16 one at ~1.7 GHz under the
+// board's power limit, and the large GEMMs are power limited.  Lane l holds index l % 16 and
+// 8 consecutive k at 8 (l / 16) of both operands; the result block gives lane l rows
+// 4 (l / 16) .. +3 of column l % 16.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <class T, int MS> struct AccT { using type = typename AccV<T>::type; };
+template <class T> struct AccT<T, 16> { using type = f32x4; };
+template <class T> __device__ __forceinline__ void mma16x16(f32x4 &c, uint4 a, uint4 b);
+template <> __device__ __forceinline__ void mma16x16<bf16_t>(f32x4 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                0);
+}
+template <> __device__ __forceinline__ void mma16x16<f16_t>(f32x4 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+template <class T, int MS> __device__ __forceinline__ void mma_blk(typename AccT<T, MS>::type &c, uint4 a, uint4 b) {
+    if constexpr (MS == 16)
+        mma16x16<T>(c, a, b);
+    else
+        mma16<T>(c, a, b);
+}
+
 __device__ __forceinline__ int swz_k(int row) { return (row & 7) ^ ((row >> 3) & 3); }
 // Chunk swizzle of M/N-major rows.  16-bit: {0, 4, 10, 14}[k & 3]; 8-bit: 2 (k & 7), which
 // puts the 8 k-rows x 2 chunks that a 32-lane slice of one ds_read_b64_tr_b8 touches on 16
@@ -153,14 +177,23 @@ template <int CPR, int ES> __device__ __forceinline__ int swz_mn(int k) {
         return (2 * (k & 7)) & (CPR - 1);
     }
 }
+// The same for the 16 x 16 x 32 fragments of 16-bit M/N-major rows: a 32-lane slice of one
+// ds_read_b64_tr_b16 reads k-rows k0 + {0..3} and k0 + 8 + {0..3} of the same 16 columns (two
+// chunks), so the swizzle 4 (k & 3) + 2 ((k >> 3) & 1) spreads those 8 rows x 2 chunks over 16
+// distinct 16-byte bank groups.  It ignores k bits 2 and 5, which the per-read offsets add.
+template <int CPR> __device__ __forceinline__ int swz_mn16(int k) {
+    static_assert(CPR >= 16, "rows of at least 256 bytes");
+    return 4 * (k & 3) + 2 * ((k >> 3) & 1);
+}
 
 __device__ __forceinline__ MB_LDS char *lds_ptr(const char *p) { return (MB_LDS char *)(MB_LDS void *)p; }
 __device__ __forceinline__ uint32_t lds_addr(const char *p) {
     return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_ptr(p));
 }
 
-// One operand tile: ROWS (M or N) x 128 bytes of K (64 16-bit or 128 8-bit elements).
-template <int ROWS, int NW, bool KC, int ES = 2> struct Tile16 {
+// One operand tile: ROWS (M or N) x 128 bytes of K (64 16-bit or 128 8-bit elements), read as
+// fragments of MS x MS MFMA blocks (MS = 32: 32 x 32 x 16 / 32 x 32 x 32; MS = 16: 16 x 16 x 32).
+template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
     static constexpr int BYTES = ROWS * 128;
     static constexpr int SEGS = BYTES / 1024;      // 1 KiB direct-load segments
     static constexpr int PER_WAVE = (SEGS + NW - 1) / NW;
@@ -168,6 +201,13 @@ template <int ROWS, int NW, bool KC, int ES = 2> struct Tile16 {
     static constexpr int CPR = RB / 16;            // MN-major chunks per row
     static constexpr int EPC = 16 / ES;            // elements per 16-byte chunk
     static_assert(ROWS % 32 == 0 && (KC || RB >= (ES == 2 ? 128 : 64)), "tile rows");
+    static_assert(MS == 32 || (MS == 16 && ES == 2), "16 x 16 blocks are 16-bit only");
+    __device__ __forceinline__ static int swz(int k) {
+        if constexpr (MS == 16)
+            return swz_mn16<CPR>(k);
+        else
+            return swz_mn<CPR, ES>(k);
+    }
 
     // Byte offset (relative to the resource base = element (row0, k0)) of the chunk a lane
     // loads for segment `seg`, or kOOB.
@@ -181,7 +221,7 @@ template <int ROWS, int NW, bool KC, int ES = 2> struct Tile16 {
             return (uint32_t)(((int64_t)r * ld + c * EPC) * ES);
         } else {
             const int k = byte / RB, p = (byte % RB) >> 4;
-            const int c = p ^ swz_mn<CPR, ES>(k);
+            const int c = p ^ swz(k);
             if (k >= k_left || c * EPC >= rows_left) return kOOB;
             return (uint32_t)(((int64_t)k * ld + c * EPC) * ES);
         }
@@ -205,6 +245,42 @@ template <int ROWS, int NW, bool KC, int ES = 2> struct Tile16 {
             const int kr = (lane & 15) >> 1;   // k row within the 8-row group
             const int col = row0 + 32 * j + 16 * ((lane >> 4) & 1) + 8 * (lane & 1);
             return (kr + 16 * (lane >> 5)) * RB + (((col >> 4) ^ swz_mn<CPR, ES>(kr)) << 4) + (col & 15);
+        }
+    }
+
+    // 16 x 16 x 32 fragments: lane l reads index l % 16 of block j (16 rows) and the 8 k at
+    // 32 s + 8 (l / 16).  K-major: one 16-byte chunk; M/N-major: two transposing reads of 4 k
+    // (k-row 8 (l / 16) + (l % 16) / 4 + 4 t of columns 4 (l % 4) .. +3).
+    __device__ __forceinline__ static int frag_base16(int row0, int lane, int j) {
+        if constexpr (KC) {
+            return (row0 + (lane & 15)) * 128;   // row0 is a multiple of 32
+        } else {
+            const int k = 8 * (lane >> 4) + ((lane & 15) >> 2);
+            const int col = row0 + 16 * j + 4 * (lane & 3);
+            return k * RB + (((col >> 3) ^ swz(k)) << 4) + ((col & 7) << 1);
+        }
+    }
+    __device__ __forceinline__ static uint4 frag16(const char *lds, int base, int lane, int s, int j) {
+        if constexpr (KC) {
+            const int row = 16 * (j & 1) + (lane & 15);   // the swizzle is periodic in 32 rows
+            const int chunk = (4 * s + (lane >> 4)) ^ swz_k(row);
+            return *(const uint4 *)(lds + base + j * 16 * 128 + (chunk << 4));
+        } else {
+            uint4 out;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int koff = (32 * s + 4 * t) * RB;
+                bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
+                const uint2 u = __builtin_bit_cast(uint2, v);
+                if (t == 0) {
+                    out.x = u.x;
+                    out.y = u.y;
+                } else {
+                    out.z = u.x;
+                    out.w = u.y;
+                }
+            }
+            return out;
         }
     }
 
@@ -260,18 +336,20 @@ __device__ __forceinline__ void tile_coords16(int pid, int tiles_m, int tiles_n,
     tn = in / gsz;
 }
 
-// Store a wave's accumulators: acc[i][j] holds the 32 x 32 block at rows mw + 32 j, columns
-// nw + 32 i; lane l owns row (l % 32) and columns 8 (r / 4) + 4 (l / 32) + r % 4 of register r.
+// Store a wave's accumulators: acc[i][j] holds the MS x MS block at rows mw + MS j, columns
+// nw + MS i; lane l owns row (l % MS) and columns 8 (r / 4) + 4 (l / MS) + r % 4 of register r
+// (MS = 32: 16 registers; MS = 16: 4).
 // Split-K slices write fp32 partial planes; otherwise the (optional) epilogue and one rounding.
-template <class T, int TM, int TN>
-__device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>::type (&acc)[TN][TM], int mw,
+template <class T, int TM, int TN, int MS = 32>
+__device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccT<T, MS>::type (&acc)[TN][TM], int mw,
                                              int nw, int bz, int ks, int lane) {
+    constexpr int NQ = MS * MS / 256;   // 4-register groups per lane
     using A = typename Tr<T>::acc;   // fp32, or the unsigned 32-bit wrapping accumulator
     // keep the store addressing from being hoisted above the main loop (where its 64-bit
     // addresses would be live across the loop and spill)
     asm volatile("" : "+s"(mw), "+s"(nw));
-    const int mrow = lane & 31;
-    const int nsub = 4 * (lane >> 5);
+    const int mrow = lane % MS;
+    const int nsub = 4 * (lane / MS);
     T *Cb = (T *)g.c + bz * g.c_bs;
     if (g.splits > 1 || g.planes) {
         A *ws = (A *)g.ws + ((int64_t)ks * g.batch + bz) * g.M * (int64_t)g.N;
@@ -280,12 +358,12 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                const int gm = mw + j * 32 + mrow;
+                const int gm = mw + j * MS + mrow;
                 if (gm >= g.M) continue;
                 A *row = ws + (int64_t)gm * g.N;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int gn = nw + i * 32 + 8 * q + nsub;
+                for (int q = 0; q < NQ; ++q) {
+                    const int gn = nw + i * MS + 8 * q + nsub;
                     if (vec && gn + 3 < g.N) {
                         A o[4];
 #pragma unroll
@@ -305,12 +383,12 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                const int gm = mw + j * 32 + mrow;
+                const int gm = mw + j * MS + mrow;
                 if (gm >= g.M) continue;
                 T *row = Cb + gm * g.c_rs;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int gn = nw + i * 32 + 8 * q + nsub;
+                for (int q = 0; q < NQ; ++q) {
+                    const int gn = nw + i * MS + 8 * q + nsub;
                     if (gn + 3 < g.N) {
                         T o[4];
 #pragma unroll
@@ -339,13 +417,13 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                const int gm = mw + j * 32 + mrow;
+                const int gm = mw + j * MS + mrow;
                 if (gm >= g.M) continue;
                 T *row = Cb + gm * g.c_rs;
                 const T *brow = Bb + gm * g.bias_rs;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int gn = nw + i * 32 + 8 * q + nsub;
+                for (int q = 0; q < NQ; ++q) {
+                    const int gn = nw + i * MS + 8 * q + nsub;
                     if (gn + 3 < g.N) {
                         T bv[4], o[4];
                         if (g.beta_nz) __builtin_memcpy(bv, brow + gn, 4 * sizeof(T));
@@ -375,11 +453,11 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccV<T>
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j) {
-                const int gm = mw + j * 32 + mrow;
+                const int gm = mw + j * MS + mrow;
                 if (gm >= g.M) continue;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int gn = nw + i * 32 + 8 * q + nsub;
+                for (int q = 0; q < NQ; ++q) {
+                    const int gn = nw + i * MS + 8 * q + nsub;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int n = gn + r;
@@ -705,14 +783,20 @@ hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs
 // Stage k lives in buffer k % 2 during phases 2k and 2k+1; its buffer is refilled (stage
 // k+2) from phase 2k+2 on, after both groups read it.  Each wave waits for its own prefetch
 // at the end of odd phases, before the barrier that publishes the stage.
-template <class T, bool A_KC, bool B_KC, bool KTAIL>
+//
+// MS selects the MFMA block: 32 (32 x 32 x 16 / 32 x 32 x 32 int8, 4 k-steps per stage) or 16
+// (16 x 16 x 32, 2 k-steps).  The 16 x 16 form spends less power per flop, which is what bounds
+// the large products, and runs without the L2 prefetch line: with the loads spread as here
+// the prefetch only adds requests.
+template <class T, bool A_KC, bool B_KC, bool KTAIL, int MS = 32>
 __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     constexpr int BM = 256, BN = 256, WM = 2, NW = 8;
-    constexpr int WTM = 128, WTN = 64, TM = WTM / 32, TN = WTN / 32;
+    constexpr int WTM = 128, WTN = 64, TM = WTM / MS, TN = WTN / MS;
     constexpr int ES = sizeof(T);
-    constexpr int BK = 128 / ES, KSTEPS = 4;
-    using TA = Tile16<BM, NW, A_KC, ES>;
-    using TB = Tile16<BN, NW, B_KC, ES>;
+    constexpr int BK = 128 / ES, KSTEPS = MS == 16 ? 2 : 4;
+    constexpr bool PF = MS == 32;
+    using TA = Tile16<BM, NW, A_KC, ES, MS>;
+    using TB = Tile16<BN, NW, B_KC, ES, MS>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
 
     __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
@@ -750,9 +834,11 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     for (int i = 0; i < TB::PER_WAVE; ++i) offb[i] = TB::src_offset(wave + i * NW, lane, ldb, rows_b, BK);
     int fba[A_KC ? 1 : TM], fbb[B_KC ? 1 : TN];
 #pragma unroll
-    for (int j = 0; j < (A_KC ? 1 : TM); ++j) fba[j] = TA::frag_base(wm * WTM, lane, j);
+    for (int j = 0; j < (A_KC ? 1 : TM); ++j)
+        fba[j] = MS == 16 ? TA::frag_base16(wm * WTM, lane, j) : TA::frag_base(wm * WTM, lane, j);
 #pragma unroll
-    for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
+    for (int j = 0; j < (B_KC ? 1 : TN); ++j)
+        fbb[j] = MS == 16 ? TB::frag_base16(wn * WTN, lane, j) : TB::frag_base(wn * WTN, lane, j);
 
     for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
         const T *Ab = (const T *)g.a + bz * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
@@ -779,14 +865,23 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     dma16(rb, base + TA::BYTES + (wave + i * NW) * 1024,
                           TB::src_offset(wave + i * NW, lane, ldb, rows_b, kleft), kt * stepb);
             }
-            const int kp = kt + kPfDist;
-            const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
-                              : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
-            pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
+            if constexpr (PF) {
+                const int kp = kt + kPfDist;
+                const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
+                                  : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+                pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
+            }
         };
         // load `op` of prefetch(kt), in the same order: the A segments, the B segments, then the
         // L2-prefetch line (so the wait for "all but the most recent load" still works)
-        constexpr int NOPS = TA::PER_WAVE + TB::PER_WAVE + 1;
+        constexpr int NOPS = TA::PER_WAVE + TB::PER_WAVE + (PF ? 1 : 0);
+        // the wait for this wave's loads of a stage (the L2-prefetch line is left in flight)
+        auto vm_wait_stage = [&]() {
+            if constexpr (PF)
+                vm_wait_but_one();
+            else
+                vm_wait_all();
+        };
         auto prefetch_op = [&](int kt, int op) {
             const uint32_t base = smem_lds + (kt & 1) * STAGE;
             const bool edge = KTAIL && kt >= nfull;
@@ -798,7 +893,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 const int ib = op - TA::PER_WAVE, seg = wave + ib * NW;
                 dma16(rb, base + TA::BYTES + seg * 1024, edge ? TB::src_offset(seg, lane, ldb, rows_b, kleft) : offb[ib],
                       kt * stepb);
-            } else {
+            } else if constexpr (PF) {
                 const int kp = kt + kPfDist;
                 const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
                                   : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
@@ -806,13 +901,13 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             }
         };
 
-        typename AccV<T>::type acc[TN][TM];
+        typename AccT<T, MS>::type acc[TN][TM];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
             for (int j = 0; j < TM; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+                for (int r = 0; r < MS * MS / 64; ++r) acc[i][j][r] = 0;
 
         uint4 fa[KSTEPS][TM], fb[KSTEPS][TN];
         auto read_stage = [&](int kt) {
@@ -820,10 +915,13 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s) {
 #pragma unroll
-                for (int j = 0; j < TM; ++j) fa[s][j] = TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
+                for (int j = 0; j < TM; ++j)
+                    fa[s][j] = MS == 16 ? TA::frag16(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0)
+                                        : TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
 #pragma unroll
                 for (int i = 0; i < TN; ++i)
-                    fb[s][i] = TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
+                    fb[s][i] = MS == 16 ? TB::frag16(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0)
+                                        : TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
             }
         };
         auto compute_stage = [&]() {
@@ -833,12 +931,13 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
 #pragma unroll
                 for (int i = 0; i < TN; ++i)
 #pragma unroll
-                    for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
+                    for (int j = 0; j < TM; ++j) mma_blk<T, MS>(acc[i][j], fb[s][i], fa[s][j]);
             __builtin_amdgcn_s_setprio(0);
         };
         // the same MFMAs with prefetch(pk)'s loads issued one after each of the first NOPS
-        // MFMAs, so their issue (and the 5 wait states each carries) overlaps the matrix cores
-        // instead of delaying the first MFMA
+        // MFMAs (every second one for the half-length 16 x 16 MFMAs), so their issue (and the 5
+        // wait states each carries) overlaps the matrix cores instead of delaying the first MFMA
+        constexpr int PF_EVERY = MS == 16 ? 2 : 1;
         auto compute_stage_pf = [&](bool do_pf, int pk) {
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -847,11 +946,12 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 for (int i = 0; i < TN; ++i)
 #pragma unroll
                     for (int j = 0; j < TM; ++j) {
-                        mma16<T>(acc[i][j], fb[s][i], fa[s][j]);
+                        mma_blk<T, MS>(acc[i][j], fb[s][i], fa[s][j]);
                         const int idx = (s * TN + i) * TM + j;
-                        if (idx < NOPS) {   // a uniform branch; one code path keeps the registers in check
+                        // a uniform branch; one code path keeps the registers in check
+                        if (idx % PF_EVERY == 0 && idx / PF_EVERY < NOPS) {
                             __builtin_amdgcn_sched_barrier(0);
-                            if (do_pf) prefetch_op(pk, idx);
+                            if (do_pf) prefetch_op(pk, idx / PF_EVERY);
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
@@ -865,7 +965,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
 
         if (nk > 0) {
             prefetch(0);
-            vm_wait_but_one();
+            vm_wait_stage();
             phase_end();
             if (group == 0) {
                 for (int kt = 0; kt < nk; ++kt) {
@@ -873,7 +973,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     if (kt + 1 < nk) prefetch(kt + 1);
                     phase_end();
                     compute_stage();                // phase 2kt+1
-                    vm_wait_but_one();
+                    vm_wait_stage();
                     phase_end();
                 }
             } else {
@@ -881,7 +981,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 phase_end();
                 for (int kt = 0; kt < nk; ++kt) {
                     read_stage(kt);                 // phase 2kt+1
-                    vm_wait_but_one();
+                    vm_wait_stage();
                     phase_end();
                     compute_stage_pf(kt + 2 < nk, kt + 2);   // phase 2kt+2: prefetch(kt+2) inside
 
@@ -889,22 +989,23 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 }
             }
         }
-        store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        store_tile16<T, TM, TN, MS>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         __syncthreads();   // LDS reuse by the next batch iteration
     }
 }
 
 template <class T, bool KTAIL>
 hipError_t launch16pp(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    constexpr int MS = sizeof(T) == 2 ? 16 : 32;   // 16 x 16 x 32 blocks for the 16-bit types
     dim3 block(512);
     if (a_kc && b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL, MS>), grid, block, 0, st, g);
     else if (a_kc && !b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, true, false, KTAIL>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, true, false, KTAIL, MS>), grid, block, 0, st, g);
     else if (!a_kc && b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, false, true, KTAIL>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, false, true, KTAIL, MS>), grid, block, 0, st, g);
     else
-        hipLaunchKernelGGL((k_gemm16pp<T, false, false, KTAIL>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, false, false, KTAIL, MS>), grid, block, 0, st, g);
     return hipGetLastError();
 }
 
