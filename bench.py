@@ -37,7 +37,7 @@ PEAK_HBM_GBS = 8000.0
 # come from a 1 GiB copy, which reads as 512 MiB of FETCH_SIZE and 1 GiB of WRITE_SIZE):
 # profiles/gemm_bf16_8192_pmc_traffic.md and profiles/gemv_bf16_16384_pmc_traffic.md
 TRAFFIC = {
-    "gemm_bf16_8192": 2.0774e9,
+    "gemm_bf16_8192": 1.7823e9,
     "gemv_bf16_16384": 5.3745e8,
 }
 
