@@ -462,7 +462,13 @@ __global__ __launch_bounds__(256) void k_axpy_band(GemvArgs g) {
         }
     }
 }
-constexpr int kBandCH = 4, kBandU = 2;
+constexpr int kBandU = 2;
+// 16-byte chunks per thread of the column band: 4 (256 threads x 4 chunks = 16 KiB of each
+// row) where the rows are that wide, else the widest band that does not overhang the row, so
+// narrow matrices get more column blocks instead of re-read columns
+__host__ __device__ inline int band_ch(int64_t rows, int vec) {
+    return rows >= 256 * vec * 4 ? 4 : (rows >= 256 * vec * 2 ? 2 : 1);
+}
 
 template <class T, int NV> hipError_t dot_xrow_launch(const GemvArgs &g, hipStream_t st, LaunchShape *shape) {
     constexpr int R = NV >= 16 ? 2 : (NV >= 8 ? 4 : 8);
@@ -504,10 +510,16 @@ template <class T, int NV> hipError_t dot_fast_launch(const GemvArgs &g, hipStre
 
 template <class T, int NV> hipError_t axpy_fast_launch(const GemvArgs &g, hipStream_t st, LaunchShape *shape) {
     if constexpr (NV == 1) {
-        const int band = 256 * Chunk<T>::V * kBandCH;
+        const int ch = band_ch(g.rows, Chunk<T>::V);
+        const int band = 256 * Chunk<T>::V * ch;
         dim3 grid(cdiv(g.rows, band), g.splits, g.batch < 65535 ? g.batch : 65535), block(256);
         if (shape) *shape = {grid, block};
-        hipLaunchKernelGGL((k_axpy_band<T, kBandCH, kBandU>), grid, block, 0, st, g);
+        if (ch == 4)
+            hipLaunchKernelGGL((k_axpy_band<T, 4, kBandU>), grid, block, 0, st, g);
+        else if (ch == 2)
+            hipLaunchKernelGGL((k_axpy_band<T, 2, kBandU>), grid, block, 0, st, g);
+        else
+            hipLaunchKernelGGL((k_axpy_band<T, 1, kBandU>), grid, block, 0, st, g);
         return hipGetLastError();
     }
     constexpr int U = NV <= 2 ? 8 : 4;
@@ -541,7 +553,10 @@ template <class T, int NV> struct AxpyL {
 
 bool gemv_fast_dtype(int dt) { return dt == F32 || dt == F16 || dt == BF16; }
 int gemv_fast_vec(int dt) { return 16 / dtype_size(dt); }
-int gemv_axpy_band_cols(int dt, int nv) { return nv == 1 ? 256 * (16 / dtype_size(dt)) * kBandCH : 0; }
+int gemv_axpy_band_cols(int dt, int nv, int64_t rows) {
+    const int vec = 16 / dtype_size(dt);
+    return nv == 1 ? 256 * vec * band_ch(rows, vec) : 0;
+}
 
 hipError_t launch_gemv_dot_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape) {
     switch (dt) {

@@ -131,8 +131,8 @@ int gemv_axpy_vec(int dt, int nv);   // elements per lane of the vector path
 bool gemv_fast_dtype(int dt);
 int gemv_fast_vec(int dt);
 // columns one workgroup of the fast axpy kernel covers when it uses column bands (nv == 1),
-// else 0
-int gemv_axpy_band_cols(int dt, int nv);
+// else 0; the band narrows for matrices with fewer columns
+int gemv_axpy_band_cols(int dt, int nv, int64_t rows);
 hipError_t launch_gemv_dot_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_gemv_axpy_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape);
 

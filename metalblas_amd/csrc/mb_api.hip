@@ -274,12 +274,14 @@ bool plan_gemv(const Prob &p, Plan &pl) {
         const int64_t waves = ((int64_t)g.rows + 64 * vv - 1) / (64 * vv) * p.batch;
         const int cus = dev_info().cus;
         int64_t splits = (8LL * cus + waves - 1) / waves;   // about 8 waves per CU
-        const int band = fast ? gemv_axpy_band_cols(p.dt, (int)nv) : 0;
+        const int band = fast ? gemv_axpy_band_cols(p.dt, (int)nv, g.rows) : 0;
+        int64_t max_splits = (p.K + 63) / 64;
         if (band > 0) {   // column-band kernel: one 4-wave workgroup per CU
             const int64_t blocks = ((int64_t)g.rows + band - 1) / band * p.batch;
             splits = (cus + blocks - 1) / blocks;
+            // narrow matrices: slices of down to 32 rows, so the grid still covers the CUs
+            if (blocks * max_splits < cus) max_splits = (p.K + 31) / 32;
         }
-        const int64_t max_splits = (p.K + 63) / 64;
         if (splits > max_splits) splits = max_splits;
         if (splits > 256) splits = 256;
         if (splits < 1) splits = 1;

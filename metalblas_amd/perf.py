@@ -1,0 +1,239 @@
+"""Shape-sweep benchmark of ``metalblas_amd.matmul`` against ``torch.matmul`` (hipBLASLt).
+
+The counterpart of the reference's ``bench/bench_matmul.py``: the same shape groups
+(``bench/bench_matmul.py:82-101``), operand layouts (``:104-125``), per-layout correctness
+probe (``:139-145``) and a per-GPU Markdown report (``:205-259``), timed with HIP events on
+this GPU instead of wall clocks around ``torch.mps.synchronize``.
+
+    python -m metalblas_amd.perf                         # bf16, every shape group
+    python -m metalblas_amd.perf --group square --dtype fp16
+    python -m metalblas_amd.perf --layout all --check    # layout sweep with a parity check
+    python -m metalblas_amd.perf --report                # write profiles/shape_sweep_<gpu>.md
+
+Numbers are best-of-``trials`` means over ``iters`` back-to-back calls, so a
+power-limited product reports its sustained rate, not its first call.
+"""
+from __future__ import annotations
+
+import argparse
+import os
+import statistics
+import time
+
+import torch
+
+from . import dispatch as _mb
+
+# the reference's shape groups, (M, N, K) (bench/bench_matmul.py:82-101)
+SHAPES = {
+    "square": [(s, s, s) for s in (128, 256, 512, 1024, 2048, 4096)],
+    "tall": [(4096, 1024, 1024), (1024, 4096, 1024), (8192, 1024, 1024), (2048, 2048, 8192)],
+    "attn": [(4096, 4096, 64), (4096, 4096, 128), (4096, 4096, 1024)],
+    "gemv": [(1, 4096, 4096), (4096, 1, 4096), (1, 1024, 1024), (1, 32000, 4096)],
+    "llm": [(2048, 14336, 4096), (4096, 4096, 11008), (4096, 11008, 4096)],
+    "thin_m": [(96, 4096, 4096), (128, 4096, 4096), (192, 4096, 4096), (256, 4096, 4096), (128, 8192, 4096)],
+    "thin_n": [(4096, 128, 4096), (4096, 256, 4096), (8192, 128, 4096), (4096, 64, 4096), (4096, 32, 4096),
+               (4096, 16, 4096), (4096, 8, 4096)],
+    "odd": [(257, 257, 257), (1023, 1023, 1023), (4097, 4097, 4097), (511, 511, 511), (333, 444, 555)],
+}
+
+DTYPES = {
+    "fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16, "c64": torch.complex64,
+    "c32": torch.complex32, "i8": torch.int8, "u8": torch.uint8, "i16": torch.int16, "i32": torch.int32,
+    "i64": torch.int64,
+}
+
+
+def _rand(shape, dtype, gen):
+    if dtype.is_complex:
+        real = torch.float16 if dtype == torch.complex32 else torch.float32
+        re = torch.randn(shape, generator=gen, device="cuda", dtype=real)
+        im = torch.randn(shape, generator=gen, device="cuda", dtype=real)
+        return torch.complex(re.float(), im.float()).to(dtype)
+    if dtype.is_floating_point:
+        return torch.randn(shape, generator=gen, device="cuda", dtype=dtype)
+    lo = 0 if dtype == torch.uint8 else -4
+    return torch.randint(lo, 4, shape, generator=gen, device="cuda", dtype=dtype)
+
+
+# operand builders for an (r, c) matrix (bench/bench_matmul.py:104-125)
+def _rm(r, c, dt, g):
+    return _rand((r, c), dt, g)
+
+
+def _cm(r, c, dt, g):
+    return _rand((c, r), dt, g).t()
+
+
+def _rowsl(r, c, dt, g):
+    return _rand((2 * r, c), dt, g)[::2]
+
+
+def _colsl(r, c, dt, g):
+    return _rand((r, 2 * c), dt, g)[:, ::2]
+
+
+def _off(r, c, dt, g):
+    return _rand((r + 1, c + 1), dt, g)[1:, 1:]
+
+
+LAYOUTS = {
+    "rm_rm": (_rm, _rm), "rm_cm": (_rm, _cm), "cm_rm": (_cm, _rm), "cm_cm": (_cm, _cm),
+    "sliced": (_rowsl, _rowsl), "colsl": (_colsl, _colsl), "offset": (_off, _off),
+}
+
+
+def _time(fn, iters, trials, warmup):
+    """Best-of-trials mean seconds per call (HIP events on the current stream)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(trials):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        e.synchronize()
+        best = min(best, s.elapsed_time(e) * 1e-3 / iters)
+    return best
+
+
+def _plan_iters(flops):
+    # about 20 ms of work per trial, at least 5 calls
+    return max(5, min(200, int(2e-2 * 1.0e15 / max(flops, 1.0))))
+
+
+def _ok(a, b, dtype):
+    ref = torch.matmul(a.cpu().to(torch.complex128 if dtype.is_complex else
+                                  (torch.float64 if dtype.is_floating_point else torch.int64)),
+                       b.cpu().to(torch.complex128 if dtype.is_complex else
+                                  (torch.float64 if dtype.is_floating_point else torch.int64)))
+    got = _mb.matmul(a, b).cpu()
+    if not (dtype.is_floating_point or dtype.is_complex):
+        # integer products wrap in the accumulator and truncate to the input width
+        # (metalblas/integer_dispatch.py:13-19); int64 wraps in the CPU product too
+        if dtype == torch.int64:
+            return bool(torch.equal(got, ref))
+        return bool(torch.equal(got, ref.to(dtype)))
+    got = got.to(ref.dtype)
+    scale = ref.abs().max().item() or 1.0
+    tol = 2e-2 if dtype in (torch.float16, torch.bfloat16, torch.complex32) else 1e-3
+    return (got - ref).abs().max().item() <= tol * scale
+
+
+def bench_one(M, N, K, dtype, build_a=_rm, build_b=_rm, check=False, cool=0.0):
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a, b = build_a(M, K, dtype, g), build_b(K, N, dtype, g)
+    flops = 2.0 * M * N * K * (4.0 if dtype.is_complex else 1.0)
+    iters = _plan_iters(flops)
+    t0 = time.perf_counter()
+    t_torch = None
+    if dtype not in (torch.complex32,) and (dtype.is_floating_point or dtype.is_complex):
+        t_torch = _time(lambda: torch.matmul(a, b), iters, 5, 3)
+    t_mb = _time(lambda: _mb.matmul(a, b), iters, 5, 3)
+    if cool > 0:
+        time.sleep(cool * (time.perf_counter() - t0))
+    ok = _ok(a, b, dtype) if check else None
+    return flops, t_torch, t_mb, ok
+
+
+def _fmt(M, N, K, flops, t_torch, t_mb, ok, prefix=""):
+    tt = f"{t_torch * 1e3:>9.3f} {flops / t_torch / 1e12:>7.2f}" if t_torch else f"{'-':>9} {'-':>7}"
+    sp = f"{t_torch / t_mb:>5.2f}x" if t_torch else f"{'-':>6}"
+    chk = "" if ok is None else ("  ok" if ok else "  XX")
+    return f"{prefix}{M:>5} {N:>5} {K:>5} | {tt} | {t_mb * 1e3:>9.3f} {flops / t_mb / 1e12:>7.2f} | {sp}{chk}"
+
+
+HEADER = f"{'M':>5} {'N':>5} {'K':>5} | {'torch ms':>9} {'TFLOPS':>7} | {'mb ms':>9} {'TFLOPS':>7} | speedup"
+
+
+def run_group(name, shapes, dtype, layout=None, check=False, cool=0.0, out=print):
+    build_a, build_b = LAYOUTS[layout or "rm_rm"]
+    rows, speedups = [], []
+    out(f"\n=== {name}  dtype={str(dtype).replace('torch.', '')}" + (f"  layout={layout}" if layout else "") + " ===")
+    out(HEADER + ("  chk" if check else ""))
+    for (M, N, K) in shapes:
+        try:
+            flops, tt, tm, ok = bench_one(M, N, K, dtype, build_a, build_b, check, cool)
+            line = _fmt(M, N, K, flops, tt, tm, ok)
+            if tt:
+                speedups.append(tt / tm)
+        except Exception as ex:   # report and go on, like the reference's sweep
+            line = f"{M:>5} {N:>5} {K:>5} | FAILED: {type(ex).__name__}: {ex}"
+        rows.append(line)
+        out(line)
+    if speedups:
+        out(f"median speedup {statistics.median(speedups):.2f}x  (min {min(speedups):.2f}x, max {max(speedups):.2f}x)")
+    return rows, speedups
+
+
+def machine_info():
+    p = torch.cuda.get_device_properties(0)
+    return {"gpu": torch.cuda.get_device_name(0), "arch": getattr(p, "gcnArchName", "?"),
+            "cus": p.multi_processor_count, "memory_gib": round(p.total_memory / 2 ** 30),
+            "torch": torch.__version__, "hip": torch.version.hip}
+
+
+def write_report(path, dtype=torch.bfloat16, layouts=None, check=False, cool=0.0):
+    info = machine_info()
+    blocks, all_sp = [], []
+    for g, shapes in SHAPES.items():
+        lines = []
+        rows, sp = run_group(g, shapes, dtype, check=check, cool=cool, out=lines.append)
+        blocks.append("\n".join(lines))
+        all_sp += sp
+    lay_blocks = []
+    for lay in layouts or []:
+        lines = []
+        run_group("square+llm", SHAPES["square"][3:] + SHAPES["llm"], dtype, layout=lay, check=check, cool=cool,
+                  out=lines.append)
+        lay_blocks.append("\n".join(lines))
+    text = [f"# {info['gpu']} ({info['arch']}, {info['cus']} CUs, {info['memory_gib']} GiB)", "",
+            f"- torch {info['torch']}, HIP {info['hip']}",
+            f"- command: `python -m metalblas_amd.perf --report" + (" --layout " + ",".join(layouts) if layouts else "")
+            + (" --check" if check else "") + "`",
+            "- times: best of 5 trials of back-to-back calls (about 20 ms each), HIP events; "
+            "`torch` is `torch.matmul` (hipBLASLt / rocBLAS)",
+            f"- median speedup over all shapes: {statistics.median(all_sp):.2f}x" if all_sp else "", "",
+            f"## {str(dtype).replace('torch.', '')} results vs `torch.matmul`", "", "```", "\n\n".join(blocks), "```", ""]
+    if lay_blocks:
+        text += ["## Layout sweep (rm = row-major, cm = column-major view, sliced = `[::2]` rows, "
+                 "colsl = `[:, ::2]`, offset = `[1:, 1:]`)", "", "```", "\n\n".join(lay_blocks), "```", ""]
+    with open(path, "w") as f:
+        f.write("\n".join(text))
+    return path
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--dtype", default="bf16", choices=list(DTYPES) + ["all"])
+    p.add_argument("--group", default="all", choices=list(SHAPES) + ["all"])
+    p.add_argument("--layout", default=None, help="comma list of " + ",".join(LAYOUTS) + " or 'all'")
+    p.add_argument("--check", action="store_true", help="compare every result with a CPU fp64/int64 product")
+    p.add_argument("--cool", type=float, default=0.0, help="sleep this ratio of each benchmark's time after it")
+    p.add_argument("--report", action="store_true", help="write profiles/shape_sweep_<gpu>.md (bf16)")
+    args = p.parse_args(argv)
+    layouts = None
+    if args.layout:
+        layouts = list(LAYOUTS) if args.layout == "all" else args.layout.split(",")
+        bad = [x for x in layouts if x not in LAYOUTS]
+        if bad:
+            p.error(f"unknown layout(s) {bad}; choose from {list(LAYOUTS)} or 'all'")
+    if args.report:
+        root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+        gpu = machine_info()["arch"].split(":")[0]
+        path = os.path.join(root, "profiles", f"shape_sweep_{gpu}.md")
+        print("wrote", write_report(path, layouts=layouts, check=args.check, cool=args.cool))
+        return
+    dtypes = list(DTYPES.values()) if args.dtype == "all" else [DTYPES[args.dtype]]
+    groups = list(SHAPES) if args.group == "all" else [args.group]
+    for dt in dtypes:
+        for g in groups:
+            for lay in layouts or [None]:
+                run_group(g, SHAPES[g], dt, layout=lay, check=args.check, cool=args.cool)
+
+
+if __name__ == "__main__":
+    main()

@@ -179,6 +179,14 @@ def test_plan_config2_gemv_families():
     assert _lib.FAMILY_NAMES[_plan(torch.float32, torch.empty(8, n), torch.empty(n, n)).family] == "gemv_axpy"
 
 
+def test_plan_narrow_x_at_w_fills_the_cus():
+    # 4096 columns: two 2048-column bands (no band overhangs the rows), K slices of 32 rows
+    W = torch.empty(4096, 4096, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, torch.empty(1, 4096, dtype=torch.bfloat16), W)
+    assert _lib.FAMILY_NAMES[p.family] == "gemv_axpy"
+    assert p.split_k == 128 and p.workspace_bytes == 128 * 4096 * 4
+
+
 def test_plan_config4_splitk_and_batches():
     a = torch.empty(1, 128, 65536, dtype=torch.float16)
     b = torch.empty(1, 65536, 128, dtype=torch.float16)
