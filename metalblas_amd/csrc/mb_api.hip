@@ -431,6 +431,7 @@ int64_t auto_splits(const Prob &p, int64_t tiles, int bk) {
 void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const int cus = dev_info().cus;
     MfmaTile t;
+    bool thin = false;   // the thin-problem tiles below (split for two workgroups per CU)
     // a tile in the descriptor is honoured for the matrix-core backends and for AUTO (where
     // the autotuner puts the tile it measured fastest)
     const bool forced = p.tile[0] > 0 && p.tile[1] > 0;
@@ -470,6 +471,18 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
                 t = c.t;
             }
         }
+        // Thin problems (fewer 128 x 128 tiles than CUs, deep K, bf16/fp16) where the pick
+        // above runs at most one workgroup per CU: 64 x 128 tiles (128 x 64 when M > N), split
+        // over K (slices of >= 1024) to two workgroups per CU when the tiles alone do not fill
+        // the CUs.  Measured on MI355X, us (cost-model pick -> this): 256x4096x4096 31.5 -> 23.1,
+        // 8192x128x4096 31.9 -> 23.7, 128x8192x4096 29.2 -> 25.2, 512x4096x4096 36.2 -> 30.6.
+        const int64_t tiles_t = ((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * p.batch;
+        if ((p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16) && p.backend == MB_BACKEND_AUTO && p.split_req == 0 &&
+            p.K >= 2048 && ((p.M + 127) / 128) * ((p.N + 127) / 128) * p.batch < cus &&
+            tiles_t * auto_splits(p, tiles_t, bk) <= cus) {
+            t = p.M > p.N ? MfmaTile{128, 64, 2, 2} : MfmaTile{64, 128, 2, 2};
+            thin = true;
+        }
     } else {
         static const MfmaTile order[] = {{256, 256, 2, 2}, {256, 128, 2, 2}, {128, 256, 2, 2},
                                          {128, 128, 2, 2}, {128, 64, 2, 2},  {64, 128, 2, 2},
@@ -494,6 +507,16 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     const int BK = 8 * (16 / es);
     const int64_t tiles = ((p.M + t.bm - 1) / t.bm) * ((p.N + t.bn - 1) / t.bn) * p.batch;
     int64_t splits = auto_splits(p, tiles, BK);
+    if (thin) {
+        splits = 1;
+        if (tiles < cus) {
+            splits = (2LL * cus + tiles - 1) / tiles;
+            const int64_t maxs = p.K / 1024;
+            if (splits > maxs) splits = maxs;
+            if (splits > 64) splits = 64;
+            if (splits < 1) splits = 1;
+        }
+    }
     if (splits > 1) {
         int64_t chunk = (p.K + splits - 1) / splits;
         chunk = (chunk + BK - 1) / BK * BK;

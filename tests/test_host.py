@@ -187,6 +187,17 @@ def test_plan_narrow_x_at_w_fills_the_cus():
     assert p.split_k == 128 and p.workspace_bytes == 128 * 4096 * 4
 
 
+def test_plan_thin_problems_fill_two_workgroups_per_cu():
+    def plan(M, N, K):
+        p = _plan(torch.bfloat16, torch.empty(M, K, dtype=torch.bfloat16), torch.empty(K, N, dtype=torch.bfloat16))
+        return tuple(p.tile[:2]), p.split_k
+    assert plan(256, 4096, 4096) == ((64, 128), 4)     # 128 tiles x 4 K slices of 1024
+    assert plan(8192, 128, 4096) == ((128, 64), 4)
+    assert plan(512, 4096, 4096) == ((64, 128), 1)     # 256 tiles already fill the CUs
+    assert plan(128, 4096, 4096) == ((128, 64), 8)     # the cost model's split plan stays
+    assert plan(2048, 2048, 2048)[0] == (128, 128)     # not thin
+
+
 def test_plan_config4_splitk_and_batches():
     a = torch.empty(1, 128, 65536, dtype=torch.float16)
     b = torch.empty(1, 65536, 128, dtype=torch.float16)
