@@ -223,6 +223,49 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
     }
 }
 
+// 16-bit rows whose source is contiguous along the row but at any 2-byte alignment (storage
+// offsets such as the reference's 17-element offset, odd leading dimensions), copied into
+// 16-byte aligned, zero-padded destination rows: each thread writes 8 elements with one
+// 16-byte store, built from the 5 aligned source words that cover them, shifted by the row's
+// misalignment.  A word is read only when it starts before the row's end, so every read lies
+// in a page that holds a valid element.  Grid as k_pack, with 8-element chunks.
+__global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
+    const int64_t chunks = a.cols_p / 8;
+    const int64_t ci = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (ci >= chunks) return;
+    const int64_t c0 = ci * 8;
+    for (int64_t bz = blockIdx.z; bz < a.batch; bz += gridDim.z) {
+        const uint16_t *src = (const uint16_t *)a.src + bz * a.s_bs;
+        uint16_t *dst = (uint16_t *)a.dst + bz * a.d_bs;
+        for (int64_t r = blockIdx.y; r < a.rows_p; r += gridDim.y) {
+            uint32_t o[4] = {0u, 0u, 0u, 0u};
+            if (r < a.rows && c0 < a.cols) {
+                const uint16_t *row = src + r * a.s_rs;
+                const int sh = (int)((uintptr_t)(row + c0) & 2);   // 0 or 2 bytes past a word
+                const uint32_t *w = (const uint32_t *)((const char *)(row + c0) - sh);
+                const int64_t left = (a.cols - c0) * 2 + sh;   // bytes from w[0] to the row end
+                uint32_t d[5];
+#pragma unroll
+                for (int j = 0; j < 5; ++j) d[j] = 4 * j < left ? w[j] : 0u;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_alignbyte(d[k + 1], d[k], sh);
+                const int64_t valid = a.cols - c0;   // elements of this chunk inside the row
+                if (valid < 8) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (e >= valid) o[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+                }
+            }
+            uint4 v;
+            v.x = o[0];
+            v.y = o[1];
+            v.z = o[2];
+            v.w = o[3];
+            *(uint4 *)(dst + r * a.d_rs + c0) = v;
+        }
+    }
+}
+
 // Bhat expansion (CplxExpandArgs): thread per (n, k pair-block) writes the two K-adjacent
 // pairs of Bhat's columns 2n and 2n + 1; the padding k' in [2K, ld) is zero-filled.
 template <class R>
@@ -273,6 +316,13 @@ hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st) {
 hipError_t launch_pack(const PackArgs &a, hipStream_t st) {
     const int64_t inner_n = a.contig_cols ? a.cols_p : a.rows_p;
     const int64_t outer_n = a.contig_cols ? a.rows_p : a.cols_p;
+    if (a.es == 2 && a.contig_cols && a.s_cs == 1 && a.d_cs == 1 && a.cols_p % 8 == 0 && a.d_rs % 8 == 0 &&
+        ((uintptr_t)a.dst & 15) == 0 && (a.d_bs % 8) == 0) {
+        dim3 grid((unsigned)((a.cols_p / 8 + 255) / 256), (unsigned)(outer_n < 65535 ? outer_n : 65535),
+                  (unsigned)(a.batch < 65535 ? a.batch : 65535));
+        hipLaunchKernelGGL(k_pack16_rows, grid, dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)((inner_n + 1023) / 1024), (unsigned)(outer_n < 65535 ? outer_n : 65535),
               (unsigned)(a.batch < 65535 ? a.batch : 65535));
     switch (a.es) {

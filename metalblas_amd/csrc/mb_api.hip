@@ -378,24 +378,37 @@ int64_t plan_packs(Prob &p, Plan &pl, int force_kc = 0) {
     const int es = dtype_size(p.dt), E = 16 / es;
     int64_t ws = 0;
     const char *placeholder = (const char *)(uintptr_t)4096;   // aligned stand-in until run time
+    bool need[2];
+    int orients[2];
+    for (int which = 0; which < 2; ++which) {
+        const bool is_a = which == 0;
+        int orient = is_a ? a_orient(p) : b_orient(p);
+        need[which] = !operand_ok(is_a ? p.a : p.b, orient, is_a, p);
+        if (((force_kc >> which) & 1) && orient != 1) need[which] = true;
+        if (orient < 0 || ((force_kc >> which) & 1)) orient = 1;
+        if (orient == 1 && p.K % E) need[which] = true;
+        orients[which] = orient;
+    }
+    // Both operands copied: zero-pad K to a whole stage (128 bytes of K) in both copies and run
+    // the product over the padded K, so the matrix-core kernels need no K-edge handling (the
+    // K-edge variants keep more registers live; 4097^3 bf16 spends 259 us in one).
+    int64_t Kp = p.K;
+    if (need[0] && need[1] && force_kc == 0) Kp = (p.K + 128 / es - 1) / (128 / es) * (128 / es);
     for (int which = 0; which < 2; ++which) {
         const bool is_a = which == 0;
         Operand &o = is_a ? p.a : p.b;
-        int orient = is_a ? a_orient(p) : b_orient(p);
-        bool need = !operand_ok(o, orient, is_a, p);
-        if (((force_kc >> which) & 1) && orient != 1) need = true;
-        if (orient < 0 || ((force_kc >> which) & 1)) orient = 1;
-        if (orient == 1 && p.K % E) need = true;
-        if (!need) continue;
+        const int orient = orients[which];
+        if (!need[which]) continue;
         PackOp &pk = pl.pack[which];
         PackArgs &a = pk.a;
         memset(&a, 0, sizeof(a));
-        // logical matrix: A is M x K, B is K x N
+        // logical matrix: A is M x K, B is K x N; the K extent is padded to Kp with zeros
         a.rows = (int)(is_a ? p.M : p.K);
         a.cols = (int)(is_a ? p.K : p.N);
         a.contig_cols = is_a ? (orient == 1) : (orient == 0);
-        const int64_t rows_p = a.contig_cols ? a.rows : (a.rows + E - 1) / E * E;
-        const int64_t cols_p = a.contig_cols ? (a.cols + E - 1) / E * E : a.cols;
+        const int64_t rows_x = is_a ? a.rows : Kp, cols_x = is_a ? Kp : a.cols;
+        const int64_t rows_p = a.contig_cols ? rows_x : (rows_x + E - 1) / E * E;
+        const int64_t cols_p = a.contig_cols ? (cols_x + E - 1) / E * E : cols_x;
         a.rows_p = (int)rows_p;
         a.cols_p = (int)cols_p;
         a.batch = o.bs == 0 ? 1 : (int)p.batch;
@@ -411,6 +424,7 @@ int64_t plan_packs(Prob &p, Plan &pl, int force_kc = 0) {
         o = {placeholder, a.d_rs, a.d_cs, a.d_bs};
         (is_a ? p.a_padded : p.b_padded) = true;
     }
+    p.K = Kp;
     return ws;
 }
 

@@ -471,7 +471,7 @@ def _offset_view(shape, dtype, g, offset, transpose=False, ld_pad=0):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32, torch.int8, torch.uint8], ids=str)
 @pytest.mark.parametrize("case", ["offset17_a", "offset1_b", "odd_ld_a", "odd_k", "both_cm_offset",
-                                  "batched_offset"])
+                                  "batched_offset", "ref_offset_k516", "ref_offset_k517"])
 def test_unaligned_operands(dev, dtype, case):
     g = gen(17)
     M, N, K = 384, 320, 512
@@ -487,6 +487,13 @@ def test_unaligned_operands(dev, dtype, case):
     elif case == "both_cm_offset":
         a = _offset_view((M, K), dtype, g, 5, transpose=True)
         b = _offset_view((K, N), dtype, g, 3, transpose=True)
+    elif case.startswith("ref_offset"):
+        # the reference benchmark's 'offset' layout, [1:, 1:] of (rows + 1) x (cols + 1)
+        # (bench/bench_matmul.py:120-121): K = 516 gives rows alternating between word-aligned
+        # and half-word starts, K = 517 rows that end inside a 16-byte chunk
+        K = int(case[-3:])
+        a = rand((M + 1, K + 1), dtype, g)[1:, 1:]
+        b = rand((K + 1, N + 1), dtype, g)[1:, 1:]
     else:
         Bb = 3
         base = rand((9 + Bb * M * K,), dtype, g)

@@ -198,6 +198,15 @@ def test_plan_thin_problems_fill_two_workgroups_per_cu():
     assert plan(2048, 2048, 2048)[0] == (128, 128)     # not thin
 
 
+def test_plan_both_operands_copied_pad_k_to_a_stage():
+    # 4097^3 bf16: both operands are copied (odd leading dimensions); K is zero-padded to 4160
+    # (a whole 64-deep stage) in both copies: A 4097 x 4160, B 4160 x 4104
+    a = torch.empty(4097, 4097, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, a, a)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k == 1
+    assert p.workspace_bytes == (4097 * 4160 * 2 + 255) // 256 * 256 + 4160 * 4104 * 2
+
+
 def test_plan_config4_splitk_and_batches():
     a = torch.empty(1, 128, 65536, dtype=torch.float16)
     b = torch.empty(1, 65536, 128, dtype=torch.float16)
