@@ -17,8 +17,8 @@ hipError_t launch_bf16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, di
 hipError_t launch_bf16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_f16_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_f16_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
-hipError_t launch_bf16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
-hipError_t launch_f16_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_bf16_pp(bool ktail, int bn, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_f16_pp(bool ktail, int bn, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
@@ -36,8 +36,9 @@ constexpr TileEntry kTiles[] = {
     {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},   {32, 32, 1, 1, 0},
 };
 // LDS-direct family (mfma16.hpp): bf16 / fp16 / int8 / uint8; sched 1 = the ping-pong kernel
+// (256 x 128 ping-pong: bf16 / fp16 only)
 constexpr TileEntry kTiles16[] = {
-    {256, 256, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
+    {256, 256, 2, 4, 1}, {256, 128, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
     {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
     // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 and
     // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 (A K-contiguous, B
@@ -73,6 +74,7 @@ bool mfma_supported_dtype(int dt) { return dt == BF16 || dt == F16 || dt == F32 
 int mfma_k_align(int dt) { return 16 / dtype_size(dt); }
 
 bool mfma_tile_compiled(int dt, const MfmaTile &t) {
+    if ((dt == I8 || dt == U8) && t.sched == 1 && t.bn != 256) return false;   // 8-bit ping-pong: 256 x 256 only
     if (is16(dt)) return in_table(kTiles16, sizeof(kTiles16) / sizeof(kTiles16[0]), t);
     return in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t);
 }
@@ -100,8 +102,9 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
             if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256) || (t.bm == 4 && t.bn == 16))
                 return m16::launch_thin(dt, !whole, t, a_kc, b_kc, g, grid, st);
             if (t.sched == 1) {
-                if (dt == BF16) return m16::launch_bf16_pp(!whole, a_kc, b_kc, g, grid, st);
-                if (dt == F16) return m16::launch_f16_pp(!whole, a_kc, b_kc, g, grid, st);
+                if (dt == BF16) return m16::launch_bf16_pp(!whole, t.bn, a_kc, b_kc, g, grid, st);
+                if (dt == F16) return m16::launch_f16_pp(!whole, t.bn, a_kc, b_kc, g, grid, st);
+                if (t.bn != 256) return hipErrorInvalidValue;
                 return m16::launch_i8_pp(!whole, a_kc, b_kc, g, grid, st);   // int8 and uint8
             }
             if (dt == BF16)

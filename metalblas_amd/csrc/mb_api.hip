@@ -465,7 +465,8 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
             double eff;
         };
         static const Cand cands[] = {
-            {{256, 256, 2, 4, 1}, 1, 1.00}, {{256, 256, 2, 2}, 1, 0.85}, {{256, 128, 2, 2}, 1, 0.66},
+            {{256, 256, 2, 4, 1}, 1, 1.00}, {{256, 128, 2, 4, 1}, 1, 0.90}, {{256, 256, 2, 2}, 1, 0.85},
+            {{256, 128, 2, 2}, 1, 0.66},
             {{128, 256, 2, 2}, 1, 0.66}, {{128, 128, 2, 2}, 1, 0.70}, {{128, 64, 2, 2}, 2, 0.65},
             {{64, 128, 2, 2}, 2, 0.60},  {{64, 64, 2, 2}, 3, 0.40},
         };
@@ -473,6 +474,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
         double best = 1e300;
         t = {64, 64, 2, 2};
         for (const auto &c : cands) {
+            if (!mfma_tile_compiled(p.dt, c.t)) continue;   // the 256 x 128 ping-pong is 16-bit float only
             const int64_t tiles = ((p.M + c.t.bm - 1) / c.t.bm) * ((p.N + c.t.bn - 1) / c.t.bn) * p.batch;
             const int64_t s = auto_splits(p, tiles, bk);
             const int64_t wgs = tiles * s, slots = (int64_t)cus * c.occ;

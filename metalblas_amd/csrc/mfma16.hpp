@@ -788,10 +788,14 @@ hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs
 // (16 x 16 x 32, 2 k-steps).  The 16 x 16 form spends less power per flop, which is what bounds
 // the large products, and runs without the L2 prefetch line: with the loads spread as here
 // the prefetch only adds requests.
-template <class T, bool A_KC, bool B_KC, bool KTAIL, int MS = 32>
+//
+// BN = 128 (16 x 16 x 32 blocks only) halves the tile along N, for products with too few
+// 256 x 256 tiles to fill the CUs: 128 x 32 wave tiles, 48 KiB stages.
+template <class T, bool A_KC, bool B_KC, bool KTAIL, int MS = 32, int BN = 256>
 __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
-    constexpr int BM = 256, BN = 256, WM = 2, NW = 8;
-    constexpr int WTM = 128, WTN = 64, TM = WTM / MS, TN = WTN / MS;
+    static_assert(BN == 256 || (BN == 128 && MS == 16), "256 x 128 tiles use 16 x 16 x 32 blocks");
+    constexpr int BM = 256, WM = 2, NW = 8;
+    constexpr int WTM = 128, WTN = BN / 4, TM = WTM / MS, TN = WTN / MS;
     constexpr int ES = sizeof(T);
     constexpr int BK = 128 / ES, KSTEPS = MS == 16 ? 2 : 4;
     constexpr bool PF = MS == 32;
@@ -994,18 +998,18 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     }
 }
 
-template <class T, bool KTAIL>
+template <class T, bool KTAIL, int BN = 256>
 hipError_t launch16pp(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
     constexpr int MS = sizeof(T) == 2 ? 16 : 32;   // 16 x 16 x 32 blocks for the 16-bit types
     dim3 block(512);
     if (a_kc && b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL, MS>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL, MS, BN>), grid, block, 0, st, g);
     else if (a_kc && !b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, true, false, KTAIL, MS>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, true, false, KTAIL, MS, BN>), grid, block, 0, st, g);
     else if (!a_kc && b_kc)
-        hipLaunchKernelGGL((k_gemm16pp<T, false, true, KTAIL, MS>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, false, true, KTAIL, MS, BN>), grid, block, 0, st, g);
     else
-        hipLaunchKernelGGL((k_gemm16pp<T, false, false, KTAIL, MS>), grid, block, 0, st, g);
+        hipLaunchKernelGGL((k_gemm16pp<T, false, false, KTAIL, MS, BN>), grid, block, 0, st, g);
     return hipGetLastError();
 }
 
