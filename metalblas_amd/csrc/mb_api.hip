@@ -7,6 +7,7 @@
 // and 160 KB of LDS: thin products (M or N <= 16) stream the matrix once through the GEMV
 // families, aligned bf16/fp16/fp32/int8/uint8 products run on the matrix-core family, and
 // everything else on the generic tiled kernel.
+#include <algorithm>
 #include <cmath>
 #include <mutex>
 #include <utility>
@@ -477,6 +478,9 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
             if (!mfma_tile_compiled(p.dt, c.t)) continue;   // the 256 x 128 ping-pong is 16-bit float only
             const int64_t tiles = ((p.M + c.t.bm - 1) / c.t.bm) * ((p.N + c.t.bn - 1) / c.t.bn) * p.batch;
             const int64_t s = auto_splits(p, tiles, bk);
+            // the 256 x 128 ping-pong tile only unsplit: split over K it measured slower than
+            // the 128 x 128 tile (2056 x 2048 x 4096: 80.8 us at 4 slices against 51.4)
+            if (c.t.sched == 1 && c.t.bn == 128 && s > 1) continue;
             const int64_t wgs = tiles * s, slots = (int64_t)cus * c.occ;
             const int64_t rounds = (wgs + slots - 1) / slots;
             const int64_t per_cu = std::min<int64_t>(c.occ, (wgs + cus - 1) / cus);
@@ -760,12 +764,16 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     GemmArgs &g = pl.gg;
     int64_t splits;
     if (dot4) {
-        // fixed K slices of m16::kThinDot4Chunk; a persistent grid of ~2 workgroups per CU that
-        // walks the row quads, so each workgroup loads its vector slice once
+        // fixed K slices of m16::kThinDot4Chunk; a persistent grid that walks the row quads, so
+        // each workgroup loads its vector slice once: two workgroups per CU, one for matrices
+        // of 256 MiB and more.  Measured on MI355X (bf16, 8 vectors, us, two -> one per CU):
+        // 16384^2 113.3 -> 101.4, 32768 x 8192 105.7 -> 103.9, 16384 x 16384 x 12 vectors
+        // 115.6 -> 110.1; 16384 x 4096 27.9 -> 29.8, 8192^2 (6 vectors) 30.8 -> 32.3.
         splits = (q.K + m16::kThinDot4Chunk - 1) / m16::kThinDot4Chunk;
         g.k_chunk = m16::kThinDot4Chunk;
         const int64_t quads = (q.M + 3) / 4;
-        int64_t wgs = (2 * cus + splits * q.batch - 1) / (splits * q.batch);
+        const int64_t per_cu = (int64_t)q.M * q.K * dtype_size(q.dt) >= ((int64_t)256 << 20) ? 1 : 2;
+        int64_t wgs = (per_cu * cus + splits * q.batch - 1) / (splits * q.batch);
         g.persist = (int)(wgs < quads ? wgs : quads);
     } else {
         const int64_t unit = dot ? 512 : 128 / dtype_size(q.dt);
@@ -940,11 +948,7 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
     return e == hipSuccess ? MB_OK : MB_ERR_LAUNCH;
 }
 
-}  // namespace
-
-extern "C" {
-
-int mb_gemm(const mb_gemm_desc *desc, void *stream) {
+int gemm_one(const mb_gemm_desc *desc, hipStream_t stream) {
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
@@ -954,10 +958,105 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream) {
         st = make_plan(desc, pl, false);
         if (st != MB_OK) return st;
     }
-    return run_plan(pl, desc, (hipStream_t)stream, nullptr);
+    return run_plan(pl, desc, stream, nullptr);
+}
+
+// ---- edge peeling ---------------------------------------------------------------------------
+// A bf16/fp16 product whose M (or N) ends 1..16 past a multiple of 256 has a last row (column)
+// of tiles that are almost empty yet cost a whole round of matrix-core time: 4097 x 4096 x 4096
+// runs 561 256 x 128 tiles in three rounds on 256 CUs.  It runs as the core [0, M') x [0, N')
+// on whole 256 x 256 tiles plus the 1..16-row (column) strips on the GEMV or thin kernels: up
+// to three launches on the caller's stream, one after another, sharing the workspace.  Taken
+// only when the core runs 256 x 256 tiles over K >= 2048, every strip runs on a streaming
+// kernel (fast GEMV or a thin matrix-core tile) and the core copies no operand that the whole
+// product would not copy too.  Measured on MI355X (bf16, us, best whole-product tile ->
+// peeled; hipBLASLt): 4097 x 4096 x 4096 162.1 -> 117.2 (124.2), 2056 x 8192 x 4096 160.2 ->
+// 119.8 (125.8), 4096 x 4100 x 4096 185.7 -> 149.1 (134.2), 4097 x 4096 x 2048 85.9 -> 72.3
+// (67.5), 8200 x 8192 x 8192 900.3 -> 797.4 (864.9).  Smaller cores lose: 2049 x 2048 x 2048
+// on 128 x 128 tiles 30.1 -> 36.3 (the strip's launch costs more than the tiles save), and
+// 8193 x 8192 x 1024 153.4 -> 157.6.
+struct Peel {
+    int n = 0;
+    mb_gemm_desc part[3];
+};
+
+bool streaming_plan(const Plan &pl) {
+    if (pl.family == MB_FAMILY_GEMV_DOT || pl.family == MB_FAMILY_GEMV_AXPY) return pl.gemv_fast;
+    return pl.family == MB_FAMILY_MFMA && thin_tile(pl.tile);
+}
+
+bool plan_peel(const mb_gemm_desc *d, Peel &pe) {
+    if (d->backend != MB_BACKEND_AUTO || d->batch != 1 || d->split_k != 0 || d->tile[0] > 0 || d->tile[1] > 0)
+        return false;
+    if (d->dtype != MB_DTYPE_BF16 && d->dtype != MB_DTYPE_F16) return false;
+    if (d->M < 2048 || d->N < 2048 || d->K < 2048) return false;
+    const int64_t rm = d->M % 256, rn = d->N % 256;
+    const bool pm = rm >= 1 && rm <= 16, pn = rn >= 1 && rn <= 16;
+    if (!pm && !pn) return false;
+    const int64_t mm = d->M - (pm ? rm : 0), nn = d->N - (pn ? rn : 0);
+    const int64_t es = dtype_size(d->dtype);
+    auto at = [es](void *ptr, int64_t elems) { return ptr ? (void *)((char *)ptr + elems * es) : ptr; };
+    pe.n = 0;
+    mb_gemm_desc core = *d;
+    core.M = mm;
+    core.N = nn;
+    pe.part[pe.n++] = core;
+    if (pm) {   // rows [mm, M) x all N
+        mb_gemm_desc s = *d;
+        s.M = rm;
+        s.a.ptr = at(d->a.ptr, mm * d->a.row_stride);
+        s.c.ptr = at(d->c.ptr, mm * d->c.row_stride);
+        s.bias.ptr = at(d->bias.ptr, mm * d->bias.row_stride);
+        pe.part[pe.n++] = s;
+    }
+    if (pn) {   // rows [0, mm) x columns [nn, N)
+        mb_gemm_desc s = *d;
+        s.M = mm;
+        s.N = rn;
+        s.b.ptr = at(d->b.ptr, nn * d->b.col_stride);
+        s.c.ptr = at(d->c.ptr, nn * d->c.col_stride);
+        s.bias.ptr = at(d->bias.ptr, nn * d->bias.col_stride);
+        pe.part[pe.n++] = s;
+    }
+    Plan whole, pc;
+    if (make_plan(d, whole) != MB_OK || make_plan(&pe.part[0], pc) != MB_OK) return false;
+    if (pc.family != MB_FAMILY_MFMA || pc.tile.bm != 256 || pc.tile.bn != 256) return false;
+    if ((pc.pack[0].on && !whole.pack[0].on) || (pc.pack[1].on && !whole.pack[1].on)) return false;
+    for (int i = 1; i < pe.n; ++i) {
+        Plan ps;
+        if (make_plan(&pe.part[i], ps) != MB_OK || !streaming_plan(ps)) return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mb_gemm(const mb_gemm_desc *desc, void *stream) {
+    Peel pe;
+    if (desc && plan_peel(desc, pe)) {
+        for (int i = 0; i < pe.n; ++i) {
+            const int st = gemm_one(&pe.part[i], (hipStream_t)stream);
+            if (st != MB_OK) return st;
+        }
+        return MB_OK;
+    }
+    return gemm_one(desc, (hipStream_t)stream);
 }
 
 int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
+    Peel pe;
+    if (desc && plan_peel(desc, pe)) {   // the parts run one after another: the largest need
+        int64_t ws = 0;
+        for (int i = 0; i < pe.n; ++i) {
+            Plan pl;
+            const int st = make_plan(&pe.part[i], pl);
+            if (st != MB_OK) return st;
+            ws = std::max<int64_t>(ws, pl.ws_bytes);
+        }
+        return ws;
+    }
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
@@ -967,12 +1066,15 @@ int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
 int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
     if (!info) return MB_ERR_INVALID_ARG;
     Plan pl;
-    int st = make_plan(desc, pl);
+    Peel pe;
+    // a peeled product reports its core (the strips run on the GEMV / thin kernels)
+    const bool peeled = desc && plan_peel(desc, pe);
+    int st = make_plan(peeled ? &pe.part[0] : desc, pl);
     if (st != MB_OK) return st;
     memset(info, 0, sizeof(*info));
     info->family = pl.family;
     info->transposed = pl.p.transposed;
-    info->workspace_bytes = pl.ws_bytes;
+    info->workspace_bytes = peeled ? mb_gemm_workspace_bytes(desc) : pl.ws_bytes;
     info->split_k = 1;
     if (pl.family == MB_FAMILY_MFMA) {
         info->tile[0] = pl.tile.bm;

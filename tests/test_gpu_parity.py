@@ -578,3 +578,36 @@ def test_complex_matrix_cores_fused(dev, dtype):
     bb = rand((K, N), dtype, g)
     got = mb.matmul(a3.to(dev), bb.to(dev))
     assert_parity(got, a3, bb.expand(3, K, N), tag=f"complex broadcast {dtype}")
+
+
+# ---- products peeled into whole 256 x 256 tiles plus 1..16-row (column) strips --------------
+
+@pytest.mark.parametrize("case", [("bf16", 4097, 4096, 4096, None), ("fp16", 2056, 8192, 4096, None),
+                                  ("bf16", 4096, 4100, 4096, None), ("bf16", 4097, 4096, 2048, "full"),
+                                  ("fp16", 4104, 4096, 2048, "row")], ids=str)
+def test_peeled_edges(dev, case):
+    name, M, N, K, bias_kind = case
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[name]
+    g = gen(M + N)
+    a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    info = mb.kernels.plan(a, b)
+    assert info["tile"][:2] == (256, 256) and info["grid"][0] == 256, info
+    mm, nn = M - M % 256, N - N % 256
+    if bias_kind is None:
+        got = mb.matmul(_to(a, dev), _to(b, dev)).cpu()
+        ref_kw = {}
+    else:
+        bias = rand((M, N) if bias_kind == "full" else (N,), dtype, g)
+        got = mb.addmm(_to(bias, dev), _to(a, dev), _to(b, dev), beta=0.5, alpha=2.0).cpu()
+        ref_kw = {"bias": bias, "beta": 0.5, "alpha": 2.0}
+    # whole rows on both sides of the core / strip boundary, and the last row
+    for r in sorted({0, mm - 1, min(mm, M - 1), M - 1}):
+        kw = dict(ref_kw)
+        if bias_kind == "full":
+            kw["bias"] = ref_kw["bias"][r:r + 1]
+        assert_parity(got[r:r + 1], a[r:r + 1], b, tag=f"peel {case} row {r}", **kw)
+    if nn < N:   # the column strip on sampled rows
+        kw = dict(ref_kw)
+        if bias_kind is not None:
+            kw["bias"] = ref_kw["bias"][..., nn:] if bias_kind == "row" else ref_kw["bias"][:, nn:]
+        assert_parity(got[:, nn:], a, b[:, nn:], tag=f"peel {case} columns", **kw)

@@ -207,6 +207,27 @@ def test_plan_both_operands_copied_pad_k_to_a_stage():
     assert p.workspace_bytes == (4097 * 4160 * 2 + 255) // 256 * 256 + 4160 * 4104 * 2
 
 
+def test_plan_peels_a_thin_edge_off_whole_tiles():
+    # 4097 x 4096 x 4096 bf16: the core 4096^2 runs on 256 whole 256 x 256 tiles (one round)
+    # and row 4096 on the streaming GEMV; the plan reports the core, and the workspace is the
+    # largest part's (the GEMV's split-K partial planes)
+    a = torch.empty(4097, 4096, dtype=torch.bfloat16)
+    b = torch.empty(4096, 4096, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, a, b)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile)[:2] == (256, 256)
+    assert tuple(p.grid) == (256, 1, 1)
+    d = _desc(torch.bfloat16, a, b)
+    assert _lib.load().mb_gemm_workspace_bytes(ctypes.byref(d)) == p.workspace_bytes > 0
+    # not peeled: a remainder above 16 rows, an explicit tile, or strips without a streaming
+    # kernel (4097^3: every row of both operands is misaligned)
+    a2 = torch.empty(4128, 4096, dtype=torch.bfloat16)
+    assert tuple(_plan(torch.bfloat16, a2, b).grid) != (256, 1, 1)
+    p = _plan(torch.bfloat16, a, b, tile=(256, 128, 64, 2, 4, 2))
+    assert tuple(p.tile)[:2] == (256, 128)
+    a3 = torch.empty(4097, 4097, dtype=torch.bfloat16)
+    assert tuple(_plan(torch.bfloat16, a3, a3).grid) == (561, 1, 1)
+
+
 def test_plan_config4_splitk_and_batches():
     a = torch.empty(1, 128, 65536, dtype=torch.float16)
     b = torch.empty(1, 65536, 128, dtype=torch.float16)
