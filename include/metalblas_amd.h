@@ -141,7 +141,9 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream);
 int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc);
 
 /* Fill *info with the plan mb_gemm() runs when given the workspace that
- * mb_gemm_workspace_bytes() reports (without it, split-K is dropped).  Replaces the plan caches/pickers of
+ * mb_gemm_workspace_bytes() reports (without it, split-K is dropped).  A bf16/fp16 product
+ * that mb_gemm() runs as whole 256 x 256 tiles plus a 1..16-row (column) edge strip reports
+ * the tiled core; workspace_bytes is then the largest part's.  Replaces the plan caches/pickers of
  * metalblas/float_dispatch.py:484-505 (_gemm_plan) and :613-655 (_pick_mpp_tensor_tile). */
 int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info);
 
