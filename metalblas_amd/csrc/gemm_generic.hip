@@ -226,9 +226,11 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
 // 16-bit rows whose source is contiguous along the row but at any 2-byte alignment (storage
 // offsets such as the reference's 17-element offset, odd leading dimensions), copied into
 // 16-byte aligned, zero-padded destination rows: each thread writes 8 elements with one
-// 16-byte store, built from the 5 aligned source words that cover them, shifted by the row's
-// misalignment.  A word is read only when it starts before the row's end, so every read lies
-// in a page that holds a valid element.  Grid as k_pack, with 8-element chunks.
+// 16-byte store, cut out of the two aligned 16-byte source chunks that cover them (whole-chunk
+// loads: a load instruction reads 1 KiB of consecutive row bytes).  Every thread of a row
+// shares the row's misalignment (8-element chunks are 16 bytes), so the cut is wave-uniform.
+// The second chunk is read only when it starts before the row's end, so every read lies in a
+// page that holds a valid element.  Grid as k_pack, with 8-element chunks.
 __global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
     const int64_t chunks = a.cols_p / 8;
     const int64_t ci = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -241,19 +243,25 @@ __global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
             uint32_t o[4] = {0u, 0u, 0u, 0u};
             if (r < a.rows && c0 < a.cols) {
                 const uint16_t *row = src + r * a.s_rs;
-                const int sh = (int)((uintptr_t)(row + c0) & 2);   // 0 or 2 bytes past a word
-                const uint32_t *w = (const uint32_t *)((const char *)(row + c0) - sh);
-                const int64_t left = (a.cols - c0) * 2 + sh;   // bytes from w[0] to the row end
-                uint32_t d[5];
+                const int mis = (int)((uintptr_t)(row + c0) & 15);   // 0, 2, ..., 14; row-uniform
+                const uint4 *w = (const uint4 *)((const char *)(row + c0) - mis);
+                const int64_t left = (a.cols - c0) * 2 + mis;   // bytes from w[0] to the row end
+                const uint4 lo = w[0];
+                const uint4 hi = left > 16 ? w[1] : make_uint4(0u, 0u, 0u, 0u);
+                const uint32_t d[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                const int q = mis >> 2, sh = mis & 3;
+                // the 5 words from word q on, picked with uniform selects
+                uint32_t e[5];
 #pragma unroll
-                for (int j = 0; j < 5; ++j) d[j] = 4 * j < left ? w[j] : 0u;
+                for (int j = 0; j < 5; ++j)
+                    e[j] = q == 0 ? d[j] : q == 1 ? d[j + 1] : q == 2 ? d[j + 2] : d[j + 3];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_alignbyte(d[k + 1], d[k], sh);
+                for (int k = 0; k < 4; ++k) o[k] = __builtin_amdgcn_alignbyte(e[k + 1], e[k], sh);
                 const int64_t valid = a.cols - c0;   // elements of this chunk inside the row
                 if (valid < 8) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (e >= valid) o[e >> 1] &= (e & 1) ? 0x0000ffffu : 0xffff0000u;
+                    for (int x = 0; x < 8; ++x)
+                        if (x >= valid) o[x >> 1] &= (x & 1) ? 0x0000ffffu : 0xffff0000u;
                 }
             }
             uint4 v;
