@@ -133,7 +133,11 @@ typedef enum mb_family {
 /* Queue C = alpha*op(A)@op(B) + beta*bias on `stream` (a hipStream_t).
  * Replaces the kernel launches of metalblas/float_dispatch.py:745-852 (matmul),
  * :897-956 (addmm), :1049-1091 (bmm/baddbmm), metalblas/integer_dispatch.py:92-150 and
- * metalblas/complex_dispatch.py:33-144. */
+ * metalblas/complex_dispatch.py:33-144.  Plans are cached per call signature (the descriptor
+ * with pointers reduced to null-ness and their low 8 bits, workspace present or absent, current
+ * device; up to 1024 signatures, thread-safe): a repeated call skips the planner.
+ * METALBLAS_LAUNCH_CACHE=0 disables the cache; =verify replans every hit and aborts on a
+ * difference. */
 int mb_gemm(const mb_gemm_desc *desc, void *stream);
 
 /* Bytes of device scratch mb_gemm() needs for this descriptor (0 if none); negative on error.

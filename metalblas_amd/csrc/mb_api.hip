@@ -9,7 +9,11 @@
 // everything else on the generic tiled kernel.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
+#include <string>
+#include <unordered_map>
 #include <utility>
 #include <string.h>
 
@@ -49,7 +53,7 @@ struct Prob {
 struct PackOp {
     bool on = false;
     int64_t off = 0;        // byte offset of the copy in the workspace
-    PackArgs a;             // source / destination strides and extents (dst pointer set at run)
+    PackArgs a{};           // source / destination strides and extents (dst pointer set at run)
 };
 
 struct Plan {
@@ -59,17 +63,17 @@ struct Plan {
     int64_t split_off = 0;    // workspace byte offset of the split-K partial planes
     // complex product run as the real product M x 2N x 2K (CplxExpandArgs)
     bool cplx = false;
-    CplxExpandArgs cx;        // B expansion (dst set at run time)
+    CplxExpandArgs cx{};      // B expansion (dst set at run time)
     int64_t cx_off = 0;
     bool cplx_reduce = false; // real GEMM writes fp32 planes; a complex reduction applies the
-    GemmArgs cr;              // epilogue and the output strides (ws set at run time)
+    GemmArgs cr{};            // epilogue and the output strides (ws set at run time)
     int cdt = 0;              // the complex dtype
     // GEMV
-    GemvArgs gv;
+    GemvArgs gv{};
     bool gemv_dot = false;
     bool gemv_fast = false;   // streaming float kernels of gemv_fast.hip
     // MFMA / generic
-    GemmArgs gg;
+    GemmArgs gg{};
     MfmaTile tile = {0, 0, 0, 0};
     bool a_kc = false, b_kc = false;
     int64_t ws_bytes = 0;
@@ -948,17 +952,16 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
     return e == hipSuccess ? MB_OK : MB_ERR_LAUNCH;
 }
 
-int gemm_one(const mb_gemm_desc *desc, hipStream_t stream) {
-    Plan pl;
+// The plan one launch sequence runs: the workspace plan, or, when the caller's scratch is
+// missing or too small, the plan that needs none (same results).
+int plan_one(const mb_gemm_desc *desc, Plan &pl) {
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
     if (pl.ws_bytes > 0 && (!desc->workspace || desc->workspace_bytes < pl.ws_bytes)) {
-        // not enough caller scratch: the plan that needs none (same results)
         pl = Plan();
         st = make_plan(desc, pl, false);
-        if (st != MB_OK) return st;
     }
-    return run_plan(pl, desc, stream, nullptr);
+    return st;
 }
 
 // ---- edge peeling ---------------------------------------------------------------------------
@@ -1029,20 +1032,159 @@ bool plan_peel(const mb_gemm_desc *d, Peel &pe) {
     return true;
 }
 
+// ---- per-signature plan cache ---------------------------------------------------------------
+// Planning a call (normalisation, the tile cost model, the peeling trial) takes 4-20 us of host
+// time, as long as a small product's kernel.  A plan depends on the operand pointers only
+// through null-ness and alignment (every check is modulo 64 bytes or less), so mb_gemm plans
+// each call signature once, on sentinel pointers that keep each real pointer's low 8 bits, and
+// later calls relocate the cached plan's pointer fields from the sentinels to their own
+// operands.  The signature is the whole descriptor with the pointers so replaced, the workspace
+// reduced to present / absent, and the current device.  METALBLAS_LAUNCH_CACHE=0 turns the cache
+// off; METALBLAS_LAUNCH_CACHE=verify also replans every hit from the real descriptor and aborts
+// when a relocated pointer or a launch choice differs.
+
+constexpr uint64_t kSentBase = uint64_t(1) << 56;   // above every canonical host / HSA address
+constexpr uint64_t kSentSpan = uint64_t(1) << 52;   // one span per operand: a, b, c, bias
+
+struct CallPlan {
+    int n = 0;       // launch sequences: 1, or the 2-3 parts of a peeled product
+    Plan part[3];
+};
+
+int plan_call(const mb_gemm_desc *d, CallPlan &cp) {
+    Peel pe;
+    if (plan_peel(d, pe)) {
+        cp.n = pe.n;
+        for (int i = 0; i < pe.n; ++i) {
+            const int st = plan_one(&pe.part[i], cp.part[i]);
+            if (st != MB_OK) return st;
+        }
+        return MB_OK;
+    }
+    cp.n = 1;
+    return plan_one(d, cp.part[0]);
+}
+
+// Calls f on every device pointer a plan holds (all are copies of, or offsets into, the
+// descriptor's a / b / c / bias operands, or set from the workspace at run time).
+template <class F>
+void each_ptr(Plan &pl, F f) {
+    f(pl.p.a.ptr); f(pl.p.b.ptr); f(pl.p.c.ptr); f(pl.p.bias.ptr);
+    for (PackOp &pk : pl.pack) { f(pk.a.src); f(pk.a.dst); }
+    f(pl.cx.b); f(pl.cx.dst);
+    for (GemmArgs *g : {&pl.cr, &pl.gg}) { f(g->a); f(g->b); f(g->c); f(g->bias); f(g->ws); }
+    f(pl.gv.mat); f(pl.gv.x); f(pl.gv.y); f(pl.gv.bias); f(pl.gv.ws);
+}
+
+struct Reloc {
+    uint64_t sent[4], real[4];
+};
+
+template <class T>
+void relocate(T *&ptr, const Reloc &r) {
+    const uint64_t v = (uint64_t)(uintptr_t)ptr;
+    const uint64_t lo = kSentBase - kSentSpan / 2;
+    if (v < lo || v >= lo + 4 * kSentSpan) return;   // not derived from an operand
+    const int k = (int)((v - lo) / kSentSpan);
+    ptr = (T *)(uintptr_t)(v - r.sent[k] + r.real[k]);
+}
+
+int cache_mode() {   // 0 off, 1 on, 2 verify
+    static const int mode = [] {
+        const char *e = getenv("METALBLAS_LAUNCH_CACHE");
+        if (!e) return 1;
+        if (strcmp(e, "0") == 0) return 0;
+        if (strcmp(e, "verify") == 0) return 2;
+        return 1;
+    }();
+    return mode;
+}
+
+std::mutex g_cache_mu;
+std::unordered_map<std::string, CallPlan> g_cache;
+constexpr size_t kCacheCap = 1024;
+
+static_assert(sizeof(mb_gemm_desc) == 296, "mb_gemm_desc has padding: the signature would read it");
+
+// The cached plan of desc's signature, relocated to desc's operands, in cp.
+int cached_plan(const mb_gemm_desc *desc, CallPlan &cp) {
+    mb_gemm_desc canon = *desc;
+    Reloc r;
+    mb_matrix *ops[4] = {&canon.a, &canon.b, &canon.c, &canon.bias};
+    for (int k = 0; k < 4; ++k) {
+        const uint64_t real = (uint64_t)(uintptr_t)ops[k]->ptr;
+        r.real[k] = real;
+        r.sent[k] = real ? kSentBase + (uint64_t)k * kSentSpan + (real & 255) : 0;
+        ops[k]->ptr = (void *)(uintptr_t)r.sent[k];
+    }
+    canon.workspace = (void *)(uintptr_t)(desc->workspace ? 1 : 0);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    std::string key((const char *)&canon, sizeof(canon));
+    key.append((const char *)&dev, sizeof(dev));
+    bool hit = false;
+    {
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        auto it = g_cache.find(key);
+        if (it != g_cache.end()) {
+            cp = it->second;
+            hit = true;
+        }
+    }
+    if (!hit) {
+        const int st = plan_call(&canon, cp);
+        if (st != MB_OK) return st;
+        std::lock_guard<std::mutex> lk(g_cache_mu);
+        if (g_cache.size() >= kCacheCap) g_cache.clear();
+        g_cache.emplace(std::move(key), cp);
+    }
+    for (int i = 0; i < cp.n; ++i) each_ptr(cp.part[i], [&](auto *&p) { relocate(p, r); });
+    if (hit && cache_mode() == 2) {
+        CallPlan fresh;
+        const int st = plan_call(desc, fresh);
+        bool same = st == MB_OK && fresh.n == cp.n;
+        for (int i = 0; same && i < cp.n; ++i) {
+            Plan &x = cp.part[i], &y = fresh.part[i];
+            uint64_t px[32], py[32];
+            int nx = 0, ny = 0;
+            each_ptr(x, [&](auto *&p) { px[nx++] = (uint64_t)(uintptr_t)p; });
+            each_ptr(y, [&](auto *&p) { py[ny++] = (uint64_t)(uintptr_t)p; });
+            for (int j = 0; j < nx && j < ny; ++j)
+                if (px[j] != py[j])
+                    fprintf(stderr, "metalblas_amd: part %d pointer field %d: relocated %llx, fresh %llx\n", i, j,
+                            (unsigned long long)px[j], (unsigned long long)py[j]);
+            same = nx == ny && memcmp(px, py, sizeof(uint64_t) * nx) == 0 && x.family == y.family &&
+                   x.ws_bytes == y.ws_bytes && x.split_off == y.split_off && x.tile.bm == y.tile.bm &&
+                   x.tile.bn == y.tile.bn && x.tile.sched == y.tile.sched && x.gg.splits == y.gg.splits &&
+                   x.gg.k_chunk == y.gg.k_chunk && x.gv.splits == y.gv.splits && x.gemv_fast == y.gemv_fast &&
+                   x.pack[0].on == y.pack[0].on && x.pack[1].on == y.pack[1].on && x.cplx == y.cplx &&
+                   x.p.transposed == y.p.transposed;
+        }
+        if (!same) {
+            fprintf(stderr, "metalblas_amd: relocated plan differs from a fresh plan (dtype %d, %lld x %lld x %lld)\n",
+                    desc->dtype, (long long)desc->M, (long long)desc->N, (long long)desc->K);
+            abort();
+        }
+    }
+    return MB_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 int mb_gemm(const mb_gemm_desc *desc, void *stream) {
-    Peel pe;
-    if (desc && plan_peel(desc, pe)) {
-        for (int i = 0; i < pe.n; ++i) {
-            const int st = gemm_one(&pe.part[i], (hipStream_t)stream);
-            if (st != MB_OK) return st;
-        }
-        return MB_OK;
+    if (!desc) return MB_ERR_INVALID_ARG;
+    CallPlan cp;
+    const int st = cache_mode() ? cached_plan(desc, cp) : plan_call(desc, cp);
+    if (st != MB_OK) return st;
+    // the parts of a peeled product run one after another on the caller's stream and share
+    // its workspace (each part's descriptor is desc with offset operands)
+    for (int i = 0; i < cp.n; ++i) {
+        const int rs = run_plan(cp.part[i], desc, (hipStream_t)stream, nullptr);
+        if (rs != MB_OK) return rs;
     }
-    return gemm_one(desc, (hipStream_t)stream);
+    return MB_OK;
 }
 
 int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
