@@ -6,7 +6,9 @@
 // (unaligned bases, odd leading dimensions, non-unit strides on both axes).  It restates
 // the structure of shaders/int_gemm.h:41-154 (A and B staged through shared memory, a
 // TM x TN micro-tile per thread, accumulate in ACC_T, truncating store) for wave64:
-// 64x64 output tile, 256 threads as 16x16, 4x4 accumulators per thread, BK = 16.
+// BT x BT output tile (BT = 64, 32 or 16), 256 threads as 16x16, (BT/16)^2 accumulators per
+// thread, BK = 16 (64, 128 for the smaller tiles).  The small tiles serve products whose
+// 64 x 64 tiles would leave CUs idle.
 #include "launch.hpp"
 
 #include <type_traits>
@@ -15,10 +17,13 @@ namespace mb {
 
 namespace {
 
-constexpr int GBM = 64, GBN = 64, GBK = 16;
-
-template <class T>
+template <class T, int BT>
 __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
+    static_assert(BT == 16 || BT == 32 || BT == 64, "generic tile");
+    constexpr int GBM = BT, GBN = BT, TT = BT / 16;   // TT x TT outputs per thread
+    // K per LDS step: each step is a serial load -> barrier -> compute round, so the small
+    // tiles (short per-step compute) take deeper steps, 8 loads per thread per operand
+    constexpr int GBK = BT == 16 ? 128 : BT == 32 ? 64 : 16;
     using A = typename Tr<T>::acc;
     __shared__ A As[GBK][GBM + 1];
     __shared__ A Bs[GBK][GBN + 1];
@@ -35,11 +40,11 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
     for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
         const T *Ab = (const T *)g.a + bz * g.a_bs;
         const T *Bb = (const T *)g.b + bz * g.b_bs;
-        A acc[4][4];
+        A acc[TT][TT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TT; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Tr<T>::zero();
+            for (int j = 0; j < TT; ++j) acc[i][j] = Tr<T>::zero();
 
         for (int k0 = kbeg; k0 < kend; k0 += GBK) {
 #pragma unroll
@@ -65,26 +70,26 @@ __global__ __launch_bounds__(256) void k_gemm_generic(GemmArgs g) {
             __syncthreads();
 #pragma unroll
             for (int kk = 0; kk < GBK; ++kk) {
-                A av[4], bv[4];
+                A av[TT], bv[TT];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) av[i] = As[kk][ty + 16 * i];
+                for (int i = 0; i < TT; ++i) av[i] = As[kk][ty + 16 * i];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx + 16 * j];
+                for (int j = 0; j < TT; ++j) bv[j] = Bs[kk][tx + 16 * j];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < TT; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = Tr<T>::mac(acc[i][j], av[i], bv[j]);
+                    for (int j = 0; j < TT; ++j) acc[i][j] = Tr<T>::mac(acc[i][j], av[i], bv[j]);
             }
             __syncthreads();
         }
 
         T *Cb = (T *)g.c + bz * g.c_bs;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TT; ++i) {
             const int gm = m0 + ty + 16 * i;
             if (gm >= g.M) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < TT; ++j) {
                 const int gn = n0 + tx + 16 * j;
                 if (gn >= g.N) continue;
                 if (g.splits > 1) {
@@ -343,12 +348,15 @@ hipError_t launch_pack(const PackArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape) {
-    const int tiles = cdiv(g.M, GBM) * cdiv(g.N, GBN);
+hipError_t launch_generic(int dt, int bt, const GemmArgs &g, hipStream_t st, LaunchShape *shape) {
+    if (bt != 16 && bt != 32 && bt != 64) return hipErrorInvalidValue;
+    const int tiles = cdiv(g.M, bt) * cdiv(g.N, bt);
     dim3 grid(tiles, g.splits, g.batch < 65535 ? g.batch : 65535), block(256);
     if (shape) *shape = {grid, block};
     return with_dtype(dt, [&]<class T>() {
-        hipLaunchKernelGGL(k_gemm_generic<T>, grid, block, 0, st, g);
+        if (bt == 16) hipLaunchKernelGGL((k_gemm_generic<T, 16>), grid, block, 0, st, g);
+        else if (bt == 32) hipLaunchKernelGGL((k_gemm_generic<T, 32>), grid, block, 0, st, g);
+        else hipLaunchKernelGGL((k_gemm_generic<T, 64>), grid, block, 0, st, g);
         return hipGetLastError();
     });
 }

@@ -109,7 +109,8 @@ struct CplxExpandArgs {
 // gemm_generic.hip
 hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st);
 hipError_t launch_pack(const PackArgs &a, hipStream_t st);
-hipError_t launch_generic(int dt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
+// bt: the square output tile, 64, 32 or 16
+hipError_t launch_generic(int dt, int bt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st);
 namespace m16 {

@@ -74,6 +74,7 @@ struct Plan {
     bool gemv_fast = false;   // streaming float kernels of gemv_fast.hip
     // MFMA / generic
     GemmArgs gg{};
+    int gen_bt = 64;          // generic family: square output tile (64, 32 or 16)
     MfmaTile tile = {0, 0, 0, 0};
     bool a_kc = false, b_kc = false;
     int64_t ws_bytes = 0;
@@ -568,10 +569,16 @@ void plan_generic(const Prob &p, Plan &pl) {
     GemmArgs &g = pl.gg;
     fill_gemm_args(p, g);
     const int cus = dev_info().cus;
-    const int64_t tiles = ((p.M + 63) / 64) * ((p.N + 63) / 64) * p.batch;
+    auto ntiles = [&p](int64_t bt) { return ((p.M + bt - 1) / bt) * ((p.N + bt - 1) / bt) * p.batch; };
+    const int64_t tiles = ntiles(64);
     int64_t splits = 1;
+    pl.gen_bt = 64;
     if (p.split_req > 1) {
         splits = p.split_req;
+    } else if (p.split_req == 0 && tiles < cus && p.K <= 1024 && ntiles(16) >= cus) {
+        // few 64 x 64 tiles, short K: 32 x 32 or 16 x 16 tiles fill the CUs with no K slices,
+        // so no partial planes and no reduction launch (int32 256^3: 256 tiles of 16 x 16)
+        pl.gen_bt = ntiles(32) >= cus ? 32 : 16;
     } else if (p.split_req == 0 && tiles < cus && p.K >= 128) {
         // few output tiles: K slices of >= 16 (one LDS step) so that ~2 workgroups run per CU
         // (int32 256^3: 16 tiles x 16 slices instead of 16 workgroups looping over K)
@@ -910,7 +917,7 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
             }
             g.ws = wsb ? wsb + pl.split_off : nullptr;
             e = pl.family == MB_FAMILY_MFMA ? launch_mfma(pl.p.dt, pl.tile, pl.a_kc, pl.b_kc, g, st, shape)
-                                            : launch_generic(pl.p.dt, g, st, shape);
+                                            : launch_generic(pl.p.dt, pl.gen_bt, g, st, shape);
             if (e != hipSuccess) break;
             if (pl.cplx_reduce) {
                 pl.cr.ws = g.ws;
@@ -1158,7 +1165,7 @@ int cached_plan(const mb_gemm_desc *desc, CallPlan &cp) {
                    x.tile.bn == y.tile.bn && x.tile.sched == y.tile.sched && x.gg.splits == y.gg.splits &&
                    x.gg.k_chunk == y.gg.k_chunk && x.gv.splits == y.gv.splits && x.gemv_fast == y.gemv_fast &&
                    x.pack[0].on == y.pack[0].on && x.pack[1].on == y.pack[1].on && x.cplx == y.cplx &&
-                   x.p.transposed == y.p.transposed;
+                   x.p.transposed == y.p.transposed && x.gen_bt == y.gen_bt;
         }
         if (!same) {
             fprintf(stderr, "metalblas_amd: relocated plan differs from a fresh plan (dtype %d, %lld x %lld x %lld)\n",
@@ -1236,9 +1243,9 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
         info->grid[1] = pl.gg.splits;
         info->grid[2] = (int)(pl.p.batch < 65535 ? pl.p.batch : 65535);
     } else if (pl.family == MB_FAMILY_GENERIC) {
-        info->tile[0] = 64;
-        info->tile[1] = 64;
-        info->tile[2] = 16;
+        info->tile[0] = pl.gen_bt;
+        info->tile[1] = pl.gen_bt;
+        info->tile[2] = pl.gen_bt == 16 ? 128 : pl.gen_bt == 32 ? 64 : 16;
         info->split_k = pl.gg.splits;
         info->block = 256;
     } else if (pl.family == MB_FAMILY_GEMV_DOT || pl.family == MB_FAMILY_GEMV_AXPY) {

@@ -611,3 +611,31 @@ def test_peeled_edges(dev, case):
         if bias_kind is not None:
             kw["bias"] = ref_kw["bias"][..., nn:] if bias_kind == "row" else ref_kw["bias"][:, nn:]
         assert_parity(got[:, nn:], a, b[:, nn:], tag=f"peel {case} columns", **kw)
+
+
+# ---- small generic tiles (16 x 16 / 32 x 32, no K slices) -------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.int16, torch.int32, torch.int64], ids=str)
+@pytest.mark.parametrize("shape", [(256, 256, 256), (250, 270, 333), (500, 520, 700), (96, 4096, 1024)], ids=str)
+@pytest.mark.parametrize("layout", ["rr", "cc"])
+def test_int_full_range_small_tiles(dev, dtype, shape, layout):
+    """Full-range integer operands on the generic kernel's 16 x 16 and 32 x 32 tiles (products
+    whose 64 x 64 tiles would leave CUs idle and whose K is short): wraparound modulo 2^bits,
+    ragged tile edges, both operand orders, the fused integer epilogue and a batch."""
+    M, N, K = shape
+    d = mb.kernels.plan(torch.empty(M, K, dtype=dtype, device=dev), torch.empty(K, N, dtype=dtype, device=dev))
+    assert d["family"] == "generic" and d["tile"][0] in (16, 32) and d["split_k"] == 1, d
+    g = gen(91)
+    info = torch.iinfo(dtype)
+    def full(shape):
+        return torch.randint(info.min, info.max, shape, generator=g, dtype=torch.int64).to(dtype)
+    a = full((M, K)) if layout[0] == "r" else full((K, M)).t()
+    b = full((K, N)) if layout[1] == "r" else full((N, K)).t()
+    got = mb.matmul(_to(a, dev), _to(b, dev))
+    assert_parity(got, a, b, tag=f"{dtype} {shape} {layout}")
+    bias = full((N,))
+    got = mb.addmm(bias.to(dev), _to(a, dev), _to(b, dev), beta=-3, alpha=7)
+    assert_parity(got, a, b, bias=bias, beta=-3, alpha=7, tag=f"{dtype} addmm {shape} {layout}")
+    ab, bb = full((3, M // 2, K)), full((3, K, N // 2))
+    got = mb.bmm(ab.to(dev), bb.to(dev))
+    assert_parity(got, ab, bb, tag=f"{dtype} bmm {shape}")
