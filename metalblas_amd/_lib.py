@@ -216,23 +216,30 @@ def workspace_bytes(desc: MbGemmDesc) -> int:
     return n
 
 
+def _device_index(device) -> int:
+    if isinstance(device, int):
+        return device
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def _current_stream(device) -> int:
-    """Raw handle of torch's current HIP stream on ``device`` (the same stream
-    ``torch.cuda.current_stream(device).cuda_stream`` names, without building a Stream object:
-    a few microseconds per call on small products)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(idx)
+    """Raw handle of torch's current HIP stream on ``device`` (a torch.device or an index; the
+    same stream ``torch.cuda.current_stream(device).cuda_stream`` names, without building a
+    Stream object: a few microseconds per call on small products)."""
+    return torch._C._cuda_getCurrentRawStream(_device_index(device))
 
 
 def launch(desc: MbGemmDesc, nbytes: int, device) -> None:
-    """Queue the product on torch's current stream of ``device`` (the current device) with
-    ``nbytes`` of workspace from torch's stream-ordered caching allocator."""
+    """Queue the product on torch's current stream of ``device`` (the current device; a
+    torch.device or an index) with ``nbytes`` of workspace from torch's stream-ordered caching
+    allocator."""
+    idx = _device_index(device)
     ws = None
     if nbytes > 0:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
         desc.workspace = ws.data_ptr()
         desc.workspace_bytes = nbytes
-    status = load().mb_gemm(ctypes.byref(desc), _current_stream(device))
+    status = (_LIB or load()).mb_gemm(ctypes.byref(desc), torch._C._cuda_getCurrentRawStream(idx))
     if status:
         check(status)
     # ws returns to torch's caching allocator; reuse is ordered on the same stream

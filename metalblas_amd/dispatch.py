@@ -96,17 +96,15 @@ _DESC_CACHE: dict = {}
 _DESC_CACHE_CAP = 4096
 
 
-def _sig(t):
-    return None if t is None else (tuple(t.stride()), t.data_ptr() & 255)
-
-
 def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_a=False,
             conj_b=False, backend=_lib.BACKEND_AUTO, tile=None, swizzle_log=None):
     """Describe and queue one (batched) product; a/b/out/bias are 2-D or 3-D tensors."""
-    dev = out.device
-    key = (dtype, batch, M, N, K, _sig(a), _sig(b), _sig(out), _sig(bias), conj_a, conj_b,
-           epilogue, backend, tile if tile is None else tuple(tile), swizzle_log, dev.index,
-           _planner.enabled())
+    idx = out.get_device()
+    pa, pb, pc = a.data_ptr(), b.data_ptr(), out.data_ptr()
+    pbias = bias.data_ptr() if bias is not None else 0
+    key = (dtype, batch, M, N, K, a.stride(), pa & 255, b.stride(), pb & 255, out.stride(), pc & 255,
+           bias.stride() if bias is not None else None, pbias & 255, conj_a, conj_b, epilogue, backend,
+           tile if tile is None else tuple(tile), swizzle_log, idx, _planner.enabled())
     hit = _DESC_CACHE.get(key)
     if hit is None:
         desc = _lib.make_desc(dtype, batch, M, N, K, _mat(a), _mat(b), _mat(out),
@@ -114,7 +112,7 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
                               conj_a=conj_a, conj_b=conj_b, epilogue=epilogue, backend=backend,
                               tile=tile, swizzle_log=swizzle_log)
         if backend == _lib.BACKEND_AUTO and tile is None:
-            with torch.cuda.device(dev):
+            with torch.cuda.device(idx):
                 _planner.tune(desc, a, b, out, bias)
         hit = (desc, _lib.workspace_bytes(desc))
         if len(_DESC_CACHE) >= _DESC_CACHE_CAP:
@@ -122,16 +120,16 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
         _DESC_CACHE[key] = hit
     template, ws_bytes = hit
     desc = _lib.MbGemmDesc.from_buffer_copy(template)
-    desc.a.ptr = a.data_ptr()
-    desc.b.ptr = b.data_ptr()
-    desc.c.ptr = out.data_ptr()
+    desc.a.ptr = pa
+    desc.b.ptr = pb
+    desc.c.ptr = pc
     if bias is not None:
-        desc.bias.ptr = bias.data_ptr()
-    if dev.index == torch.cuda.current_device():
-        _lib.launch(desc, ws_bytes, dev)
+        desc.bias.ptr = pbias
+    if idx == torch.cuda.current_device():
+        _lib.launch(desc, ws_bytes, idx)
     else:
-        with torch.cuda.device(dev):
-            _lib.launch(desc, ws_bytes, dev)
+        with torch.cuda.device(idx):
+            _lib.launch(desc, ws_bytes, idx)
     return out
 
 
