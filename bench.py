@@ -61,12 +61,19 @@ def parse():
 # untimed GPU time before each secondary configuration's timed calls (the headline keeps the
 # driver's W warmup steps: at 0.86 ms a call they already cover the clock ramp)
 CFG_WARM_MS = 20.0
+# timed calls of each secondary configuration, at least: the timed region starts from an idle,
+# synchronised GPU, and that start costs about 100 us, which 20 calls of a 10 us product would
+# read as 5 us a call (the headline times exactly the driver's K steps)
+CFG_MIN_CALLS = 200
 
 
 def time_events(torch, fn, steps, warmup, warm_ms=0.0):
-    """ms per call of fn over `steps` calls, after `warmup` untimed calls and, when warm_ms > 0,
-    more untimed calls until the GPU has run them for warm_ms (the clock ramps up over the first
-    milliseconds of work after the host-side set-up, longer than 5 calls of a 50 us product)."""
+    """ms per call of fn over `steps` calls (at least CFG_MIN_CALLS when warm_ms > 0), after
+    `warmup` untimed calls and, when warm_ms > 0, more untimed calls until the GPU has run them
+    for warm_ms (the clock ramps up over the first milliseconds of work after the host-side
+    set-up, longer than 5 calls of a 50 us product)."""
+    if warm_ms > 0:
+        steps = max(steps, CFG_MIN_CALLS)
     for _ in range(warmup):
         fn()
     if warm_ms > 0:
@@ -342,6 +349,8 @@ def main():
         g = cfg["gemv_W@x"]
         g["roofline"]["traffic"] = TRAFFIC["gemv_bf16_16384"]
         result["configs"] = cfg
+        result["configs_timing"] = (f"each config: {args.warmup} warmup calls, {CFG_WARM_MS:g} ms of untimed "
+                                    f"calls, then {max(args.steps, CFG_MIN_CALLS)} timed calls (HIP events)")
         if result["value"] is None:
             result.update({"value": g["value"], "unit": "GB/s", "ms_per_step": g["ms"],
                            "roofline": dict(g["roofline"], achieved=g["value"], unit="GB/s")})
