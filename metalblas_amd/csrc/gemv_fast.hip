@@ -211,6 +211,82 @@ __global__ __launch_bounds__(256) void k_dot_wg(GemvArgs g) {
     }
 }
 
+// complex64 single-vector dot on the k_dot_wg stream: each 16-byte chunk of a row holds two
+// complex elements, multiplied into the row's (re, im) accumulators in fp32 with conj(W) and
+// conj(x) as signs: y = sum (wr + i sa wi)(xr + i sb xi) = sum wr xr - sa sb wi xi
+// + i (sb wr xi + sa wi xr).  Plain products only (the planner routes epilogues elsewhere).
+template <int RW, int U>
+__global__ __launch_bounds__(256) void k_cdot_wg(GemvArgs g) {
+    __shared__ float part[4][RW][2];
+    const float sa = g.conj_mat ? -1.f : 1.f, sb = g.conj_x ? -1.f : 1.f, sab = sa * sb;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int nch = g.K / 2;
+    for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z)
+    for (int row0 = blockIdx.x * RW; row0 < g.rows; row0 += gridDim.x * RW) {
+        const c64_t *mat = (const c64_t *)g.mat + bz * g.mat_bs;
+        const uint4 *xp = (const uint4 *)((const c64_t *)g.x + bz * g.x_bs);
+        const uint4 *mp[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) mp[r] = (const uint4 *)(mat + (int64_t)min(row0 + r, g.rows - 1) * g.mat_ld);
+        float re[RW], im[RW];
+#pragma unroll
+        for (int r = 0; r < RW; ++r) re[r] = im[r] = 0.f;
+        auto mac = [&](int r, uint4 m, uint4 x) {
+            const float w0r = __uint_as_float(m.x), w0i = __uint_as_float(m.y);
+            const float w1r = __uint_as_float(m.z), w1i = __uint_as_float(m.w);
+            const float x0r = __uint_as_float(x.x), x0i = __uint_as_float(x.y);
+            const float x1r = __uint_as_float(x.z), x1i = __uint_as_float(x.w);
+            re[r] = __builtin_fmaf(w0r, x0r, re[r]);
+            re[r] = __builtin_fmaf(w0i, -sab * x0i, re[r]);
+            re[r] = __builtin_fmaf(w1r, x1r, re[r]);
+            re[r] = __builtin_fmaf(w1i, -sab * x1i, re[r]);
+            im[r] = __builtin_fmaf(w0r, sb * x0i, im[r]);
+            im[r] = __builtin_fmaf(w0i, sa * x0r, im[r]);
+            im[r] = __builtin_fmaf(w1r, sb * x1i, im[r]);
+            im[r] = __builtin_fmaf(w1i, sa * x1r, im[r]);
+        };
+        int c = t;
+        for (; c + 256 * (U - 1) < nch; c += 256 * U) {
+            uint4 m[RW][U], xv[U];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) m[r][u] = ld_stream(mp[r] + c + 256 * u);
+#pragma unroll
+            for (int u = 0; u < U; ++u) xv[u] = xp[c + 256 * u];
+#pragma unroll
+            for (int r = 0; r < RW; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) mac(r, m[r][u], xv[u]);
+        }
+        for (; c < nch; c += 256) {
+            const uint4 xv = xp[c];
+#pragma unroll
+            for (int r = 0; r < RW; ++r) mac(r, ld_stream(mp[r] + c), xv);
+        }
+#pragma unroll
+        for (int r = 0; r < RW; ++r) {
+            re[r] = wave_sum(re[r]);
+            im[r] = wave_sum(im[r]);
+        }
+        if (lane == 0)
+#pragma unroll
+            for (int r = 0; r < RW; ++r) {
+                part[w][r][0] = re[r];
+                part[w][r][1] = im[r];
+            }
+        __syncthreads();
+        if (t < RW && row0 + t < g.rows) {
+            const int row = row0 + t;
+            c64_t v;
+            v.re = (part[0][t][0] + part[1][t][0]) + (part[2][t][0] + part[3][t][0]);
+            v.im = (part[0][t][1] + part[1][t][1]) + (part[2][t][1] + part[3][t][1]);
+            ((c64_t *)g.y + bz * g.y_bs)[row * g.y_is] = v;
+        }
+        __syncthreads();
+    }
+}
+
 // dot family with X stored k-major (X(k, v) at x[k*x_ks + v], NV values contiguous per k):
 // the thin side of W @ X for a row-major X.  Each lane loads the V k-rows of X that match its
 // 16-byte matrix chunk (V loads of NV elements) and reuses them for R matrix rows.
@@ -559,6 +635,17 @@ int gemv_axpy_band_cols(int dt, int nv, int64_t rows) {
 }
 
 hipError_t launch_gemv_dot_fast(int dt, const GemvArgs &g, hipStream_t st, LaunchShape *shape) {
+    if (dt == C64) {   // one vector, no epilogue (plan_gemv): the k_dot_wg stream
+        if (g.nv != 1 || g.epilogue) return hipErrorInvalidValue;
+        constexpr int RW = 2, U = 4;
+        int blocks = cdiv(g.rows, RW);
+        const int cap = g.grid_cap > 0 ? 2 * g.grid_cap : 0;
+        if (cap > 0 && blocks > cap) blocks = cap;
+        dim3 grid(blocks, 1, g.batch < 65535 ? g.batch : 65535), block(256);
+        if (shape) *shape = {grid, block};
+        hipLaunchKernelGGL((k_cdot_wg<RW, U>), grid, block, 0, st, g);
+        return hipGetLastError();
+    }
     switch (dt) {
         case F32: return by_nv<float, DotL>(g, st, shape);
         case F16: return by_nv<f16_t, DotL>(g, st, shape);

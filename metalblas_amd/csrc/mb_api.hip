@@ -256,6 +256,8 @@ bool plan_gemv(const Prob &p, Plan &pl) {
         ok = ok && (nv == 1 || (g.x_vs * es) % 16 == 0);
         g.vec_ok = ok;
         fast = ok && gemv_fast_dtype(p.dt);
+        // complex64, one vector, no epilogue: the complex k_dot_wg stream (k_cdot_wg)
+        if (p.dt == MB_DTYPE_C64 && ok && nv == 1 && !p.epilogue) fast = true;
         // X with its nv values contiguous per k (row-major thin X): exact power-of-two nv,
         // every k-row aligned to nv elements
         const int bucket = gemv_nv_bucket((int)nv);

@@ -639,3 +639,28 @@ def test_int_full_range_small_tiles(dev, dtype, shape, layout):
     ab, bb = full((3, M // 2, K)), full((3, K, N // 2))
     got = mb.bmm(ab.to(dev), bb.to(dev))
     assert_parity(got, ab, bb, tag=f"{dtype} bmm {shape}")
+
+
+# ---- complex64 GEMV on the workgroup-wide row stream (k_cdot_wg, conj as signs) ----------------
+
+@pytest.mark.parametrize("conj", ["none", "a", "b", "ab"])
+@pytest.mark.parametrize("shape", [(8192, 8192), (1001, 2048), (3, 512), (4096, 4095), (1, 512)], ids=str)
+def test_complex64_gemv_streaming(dev, shape, conj):
+    M, K = shape
+    g = gen(M + K)
+    a = rand((M, K), torch.complex64, g)
+    x = rand((K,), torch.complex64, g)
+    A, X = a.to(dev), x.to(dev)
+    if "a" in conj:
+        a, A = a.conj(), A.conj()
+    if "b" in conj:
+        x, X = x.conj(), X.conj()
+    info = mb.kernels.plan(A.resolve_conj(), X.resolve_conj()[:, None])
+    if K % 2 == 0:   # the streaming kernel reads 16-byte chunks (two complex elements) of a row
+        assert info["family"] == "gemv_dot" and info["tile"][0] == 1 and info["tile"][2] == 1, info
+    got = mb.matmul(A, X)
+    assert got.shape == (M,)
+    assert_parity(got[:, None], a, x[:, None], tag=f"complex gemv {shape} conj={conj}")
+    out = torch.empty(M, dtype=torch.complex64, device=dev)
+    mb.matmul(A, X, out=out)
+    assert torch.equal(out.cpu(), got.cpu())
