@@ -250,9 +250,12 @@ def _matmul_nd(a, b, out=None):
     if a.ndim >= 3 and b.ndim == 2 and not b_vec and out is None and a.numel() and K:
         # (..., M, K) @ (K, N) with the leading dims of A foldable into its rows: one 2-D
         # product of (batch*M) x K, the same sums as the broadcast batches below, one launch
-        a2 = a.reshape(-1, K)
-        if a2.data_ptr() == a.data_ptr() and a2._base is not None:
-            return matmul(a2, b).reshape(*a.shape[:-1], N)
+        try:
+            a2 = a.view(-1, K)   # raises when the leading dims do not fold without a copy
+        except RuntimeError:
+            a2 = None
+        if a2 is not None:
+            return matmul(a2, b).view(*a.shape[:-1], N)
     batch = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
     if batch:
         size = prod(batch)
