@@ -249,6 +249,32 @@ def test_plan_config5_int8_and_complex():
     assert _lib.FAMILY_NAMES[_plan(torch.complex64, A, x).family] == "gemv_dot"
 
 
+def test_plan_config1_int32_small_generic_tiles():
+    """Short-K integer products that 64 x 64 tiles leave underfilled run unsplit on 16 x 16 or
+    32 x 32 tiles (one launch, no workspace); deep K keeps the K slices."""
+    def gp(M, N, K):
+        a, b = torch.empty(M, K, dtype=torch.int32), torch.empty(K, N, dtype=torch.int32)
+        p = _plan(torch.int32, a, b)
+        return _lib.FAMILY_NAMES[p.family], tuple(p.tile[:3]), p.split_k, p.workspace_bytes
+    assert gp(256, 256, 256) == ("generic", (16, 16, 128), 1, 0)
+    assert gp(512, 512, 512) == ("generic", (32, 32, 64), 1, 0)
+    fam, tile, split, ws = gp(256, 256, 4096)
+    assert tile == (64, 64, 16) and split > 1 and ws == split * 256 * 256 * 4
+    assert gp(1024, 1024, 1024)[1:3] == ((64, 64, 16), 1)
+    assert gp(64, 96, 80)[1:3] == ((64, 64, 16), 1)
+
+
+def test_plan_complex_gemv_streams_rows():
+    """complex64 W @ x with W K-contiguous and even K runs the workgroup-wide row stream (fast
+    GEMV, one vector, no workspace); odd K keeps the generic complex dot kernel."""
+    for M, K, fast in ((8192, 8192, 1), (3, 512, 1), (4096, 4095, 0)):
+        A = torch.empty(M, K, dtype=torch.complex64)
+        x = torch.empty(K, 1, dtype=torch.complex64)
+        p = _plan(torch.complex64, A, x)
+        assert _lib.FAMILY_NAMES[p.family] == "gemv_dot" and p.tile[0] == 1 and p.tile[2] == fast
+        assert p.workspace_bytes == 0
+
+
 def test_plan_k0_fill_and_empty():
     a = torch.empty(4, 0, dtype=torch.bfloat16)
     b = torch.empty(0, 5, dtype=torch.bfloat16)
