@@ -104,10 +104,16 @@ typedef struct mb_gemm_desc {
     int64_t alpha_int, beta_int;  /* integer dtypes: taken modulo 2^(accumulator bits) */
     int32_t tile[8];      /* 0-filled = auto; see MB_BACKEND_* for the meaning */
     int32_t split_k;      /* 0 = auto, 1 = off, >1 = number of K slices (matrix-core family) */
-    int32_t flags;        /* reserved, must be 0 */
+    int32_t flags;        /* 0, or MB_FLAG_DRY_RUN; other bits are rejected */
     void *workspace;      /* caller-provided device scratch (see mb_gemm_workspace_bytes) */
     int64_t workspace_bytes;
 } mb_gemm_desc;
+
+/* desc->flags: plan the call exactly as mb_gemm() would (through its per-signature plan cache,
+ * including METALBLAS_LAUNCH_CACHE=verify) and return MB_OK without queuing any work.  For
+ * host-side tests of the planner and the cache: no kernel is launched, so a descriptor's
+ * pointers need not be valid device memory. */
+#define MB_FLAG_DRY_RUN 1
 
 /* What the planner chose for a descriptor (for tests, the autotuner and reports). */
 typedef struct mb_plan_info {

@@ -50,6 +50,9 @@ ERR_NO_DEVICE = -6
 ERR_GEMV_SHAPE = -7
 ERR_BAD_BACKEND = -8
 
+# mb_gemm_desc.flags bits
+FLAG_DRY_RUN = 1
+
 # mb_query codes
 QUERY_ABI_VERSION, QUERY_HAS_MATRIX_CORES, QUERY_CU_COUNT, QUERY_GFX_ARCH, QUERY_LDS_BYTES = range(5)
 
@@ -149,7 +152,7 @@ def matrix(t, rs=None, cs=None, bs=0) -> MbMatrix:
 
 def make_desc(dtype, batch, M, N, K, a, b, c, bias=None, *, conj_a=False, conj_b=False,
               epilogue=None, backend=BACKEND_AUTO, tile=None, swizzle_log=None,
-              split_k=0) -> MbGemmDesc:
+              split_k=0, flags=0) -> MbGemmDesc:
     """Build a descriptor.  a/b/c/bias are (tensor, row_stride, col_stride, batch_stride).
 
     epilogue: None or (beta, alpha, beta_nz, alpha_nz) with beta/alpha already cast the way
@@ -181,6 +184,7 @@ def make_desc(dtype, batch, M, N, K, a, b, c, bias=None, *, conj_a=False, conj_b
         for i, v in enumerate(vals):
             d.tile[i] = v
     d.split_k = int(split_k)
+    d.flags = int(flags)
     return d
 
 

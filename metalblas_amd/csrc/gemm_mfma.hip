@@ -84,7 +84,9 @@ int mfma_list_tiles(int dt, MfmaTile *out, int cap) {
     const int cnt = is16(dt) ? (int)(sizeof(kTiles16) / sizeof(kTiles16[0])) : (int)(sizeof(kTiles) / sizeof(kTiles[0]));
     int n = 0;
     for (int i = 0; i < cnt; ++i) {
-        if (n < cap) out[n] = {tb[i].bm, tb[i].bn, tb[i].wm, tb[i].wn, tb[i].sched};
+        const MfmaTile t{tb[i].bm, tb[i].bn, tb[i].wm, tb[i].wn, tb[i].sched};
+        if (!mfma_tile_compiled(dt, t)) continue;   // e.g. the 8-bit ping-pong exists at 256 x 256 only
+        if (n < cap) out[n] = t;
         ++n;
     }
     return n;

@@ -124,7 +124,7 @@ int normalise(const mb_gemm_desc *d, Prob &p) {
     if (d->backend < 0 || d->backend >= MB_BACKEND_COUNT) return MB_ERR_BAD_BACKEND;
     if (d->batch < 0 || d->M < 0 || d->N < 0 || d->K < 0) return MB_ERR_INVALID_ARG;
     if (d->batch > kI32Max || d->M > kI32Max || d->N > kI32Max || d->K > kI32Max) return MB_ERR_INVALID_ARG;
-    if (d->flags != 0) return MB_ERR_INVALID_ARG;
+    if (d->flags & ~MB_FLAG_DRY_RUN) return MB_ERR_INVALID_ARG;
     p.dt = d->dtype;
     p.batch = d->batch;
     p.M = d->M;
@@ -1187,6 +1187,7 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream) {
     CallPlan cp;
     const int st = cache_mode() ? cached_plan(desc, cp) : plan_call(desc, cp);
     if (st != MB_OK) return st;
+    if (desc->flags & MB_FLAG_DRY_RUN) return MB_OK;
     // the parts of a peeled product run one after another on the caller's stream and share
     // its workspace (each part's descriptor is desc with offset operands)
     for (int i = 0; i < cp.n; ++i) {

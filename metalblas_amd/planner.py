@@ -13,10 +13,11 @@ Restates the reference's autotuner (metalblas/float_dispatch.py:411-481: ``_prob
   * the winner is cached per (device, dtype, batch, M, N, K, layout, alignment) key; with
     ``METALBLAS_PLAN_CACHE=<file>`` the cache persists as JSON across processes.
 
-Tuning is opt-in here: ``METALBLAS_AUTOTUNE=1`` enables it, anything else (or unset) keeps the
-C planner's static plans.  The reference tunes by default and reads ``METALBLAS_AUTOTUNE=0``
-as off (float_dispatch.py:156); this build keeps the static plans by default, since they
-are what its GPU test suite exercises.  Timing uses HIP events on torch's current stream.
+As in the reference (float_dispatch.py:156), tuning is on unless ``METALBLAS_AUTOTUNE=0``,
+which keeps the C planner's static plans.  The switch is read at each call.  Candidates are
+timed into a scratch output with the real output's strides and pointer alignment (so a
+column-major or offset ``out`` is tuned as the transposed / offset problem it runs as), with HIP
+events on torch's current stream.
 """
 from __future__ import annotations
 
@@ -33,12 +34,15 @@ MARGIN = 0.03
 _MIN_WORK = 1 << 27          # batch*M*N*K below this is not worth timing
 _PLANS: dict = {}
 _LOCK = threading.Lock()
-_CACHE_PATH = os.environ.get("METALBLAS_PLAN_CACHE")
-_loaded = False
+_loaded_from: set = set()     # plan-cache files already merged into _PLANS
 
 
 def enabled() -> bool:
-    return os.environ.get("METALBLAS_AUTOTUNE", "0") == "1"
+    return os.environ.get("METALBLAS_AUTOTUNE", "1") != "0"
+
+
+def _cache_path():
+    return os.environ.get("METALBLAS_PLAN_CACHE") or None
 
 
 def probe_params(M, N, K):
@@ -52,29 +56,33 @@ def probe_params(M, N, K):
 
 
 def _load_cache():
-    global _loaded
-    if _loaded:
+    """Merge the plan-cache file named by METALBLAS_PLAN_CACHE into the in-memory plans (once
+    per file)."""
+    path = _cache_path()
+    if not path or path in _loaded_from:
         return
-    _loaded = True
-    if not _CACHE_PATH or not os.path.exists(_CACHE_PATH):
+    _loaded_from.add(path)
+    if not os.path.exists(path):
         return
     try:
-        with open(_CACHE_PATH) as f:
+        with open(path) as f:
             data = json.load(f)
-        for k, v in data.items():
-            _PLANS[k] = tuple(v) if v is not None else None
+        with _LOCK:
+            for k, v in data.items():
+                _PLANS.setdefault(k, tuple(v) if v is not None else None)
     except (OSError, ValueError):
         pass
 
 
 def _save_cache():
-    if not _CACHE_PATH:
+    path = _cache_path()
+    if not path:
         return
-    tmp = _CACHE_PATH + ".tmp"
+    tmp = f"{path}.{os.getpid()}.tmp"
     try:
         with open(tmp, "w") as f:
             json.dump({k: (list(v) if v is not None else None) for k, v in _PLANS.items()}, f)
-        os.replace(tmp, _CACHE_PATH)
+        os.replace(tmp, path)
     except OSError:
         pass
 
@@ -88,8 +96,10 @@ def _key(desc, device) -> str:
 
 
 def clear():
+    """Forget every tuned plan (and which plan-cache files were read)."""
     with _LOCK:
         _PLANS.clear()
+        _loaded_from.clear()
 
 
 def cached() -> dict:
@@ -134,6 +144,18 @@ def tune(desc, a, b, out, bias=None) -> None:
             desc.tile[i] = int(v)
 
 
+def _like_out(out):
+    """A scratch tensor with ``out``'s shape and strides whose data pointer has the same
+    alignment modulo 256 bytes, so the candidates run the plan the real output runs (the plan
+    depends on the output's layout and on its pointer's low bits)."""
+    es = out.element_size()
+    span = 1 + sum((n - 1) * abs(st) for n, st in zip(out.shape, out.stride()))
+    shift = (out.data_ptr() % 256) // es
+    base = torch.empty(span + 256 // es, dtype=out.dtype, device=out.device)
+    shift = (shift - (base.data_ptr() % 256) // es) % (256 // es)
+    return base.as_strided(out.shape, out.stride(), shift)
+
+
 def _autotune(desc, out):
     info = _lib.plan(desc)
     if _lib.FAMILY_NAMES.get(info.family) != "mfma":
@@ -143,8 +165,8 @@ def _autotune(desc, out):
         return None
     lib = _lib.load()
     stream = torch.cuda.current_stream(out.device).cuda_stream
-    scratch = torch.empty_like(out, memory_format=torch.contiguous_format)
-    ref = torch.empty_like(scratch)
+    scratch = _like_out(out)
+    ref = _like_out(out)
 
     def runner(tile, dst):
         d = _lib.MbGemmDesc.from_buffer_copy(desc)

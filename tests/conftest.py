@@ -9,8 +9,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 warnings.filterwarnings("ignore", message="ComplexHalf support is experimental")
-# the autotuner times candidates; parity tests exercise the static plans unless a test opts in
-os.environ.setdefault("METALBLAS_AUTOTUNE", "0")
+# the suite runs under the library's defaults, as a user's process would: the one-shot autotuner
+# is on unless the environment says METALBLAS_AUTOTUNE=0 (tests that need one state set it)
 
 
 def pytest_configure(config):

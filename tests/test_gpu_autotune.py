@@ -1,0 +1,115 @@
+"""The one-shot autotuner on the GPU (metalblas/float_dispatch.py:411-481 _probe_params /
+_fastest / _autotune_mppt, :986-1019 _autotune_bmm), and the persistent plan cache.
+
+Each tuned product is checked against the CPU oracle; the plan cache written by the first
+tuning must, after every in-memory plan is forgotten, be read back and reused without timing
+anything, giving bit-identical outputs.  Also: the drop-in import name, and ``swizzle_log=``.
+"""
+import json
+
+import pytest
+import torch
+
+import metalblas_amd as mb
+from metalblas_amd import dispatch, planner
+from helpers import assert_parity, assert_parity_full, gen, rand
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(dev):
+    """(tag, call, check-args): the BASELINE shapes the reference tunes, plus a complex64
+    product (its four real products are tuned through the float GEMM in the reference)."""
+    g = gen(21)
+    a = torch.randn(2048, 4096, generator=g).to(torch.bfloat16).to(dev)
+    b = torch.randn(4096, 2048, generator=g).to(torch.bfloat16).to(dev)
+    bcm = torch.randn(2048, 4096, generator=g).to(torch.bfloat16).to(dev).t()
+    out_cm = torch.empty(2048, 2048, dtype=torch.bfloat16, device=dev).t()   # column-major out
+    a3 = torch.randn(8, 512, 256, generator=g).to(torch.float16).to(dev)
+    b3 = torch.randn(8, 256, 512, generator=g).to(torch.float16).to(dev)
+    ca = rand((1024, 1024), torch.complex64, g).to(dev)
+    cb = rand((1024, 1024), torch.complex64, g).to(dev)
+    ia = torch.randint(-4, 5, (2048, 2048), generator=g, dtype=torch.int8).to(dev)
+    ib = torch.randint(-4, 5, (2048, 2048), generator=g, dtype=torch.int8).to(dev)
+    return [
+        ("bf16 2048x4096x2048 rm_rm", lambda: mb.matmul(a, b), (a, b)),
+        ("bf16 2048x4096x2048 rm_cm", lambda: mb.matmul(a, bcm), (a, bcm)),
+        ("bf16 2048x4096x2048 column-major out", lambda: mb.matmul(a, b, out=out_cm), (a, b)),
+        ("fp16 bmm 8x512x512x256", lambda: mb.bmm(a3, b3), (a3, b3)),
+        ("complex64 1024^3 conj(A)", lambda: mb.matmul(ca.conj(), cb), (ca.conj(), cb)),
+        ("int8 2048^3", lambda: mb.matmul(ia, ib), (ia, ib)),
+    ]
+
+
+def test_tuned_plans_match_oracle_and_persist(dev, tmp_path, monkeypatch):
+    path = tmp_path / "plans.json"
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
+    monkeypatch.setenv("METALBLAS_PLAN_CACHE", str(path))
+    planner.clear()
+    dispatch._DESC_CACHE.clear()
+    cases = _cases(dev)
+    first = []
+    for tag, call, (a, b) in cases:
+        print("tuning", tag, flush=True)
+        got = call()
+        torch.cuda.synchronize()
+        assert_parity_full(got, a, b, rows=12, tag=f"tuned {tag}")
+        first.append(got.clone())
+    tuned = planner.cached()
+    assert len(tuned) == len(cases), tuned           # one plan key per case
+    assert path.exists()
+    on_disk = json.loads(path.read_text())
+    assert set(on_disk) == set(tuned)
+
+    # a fresh process's view: no plan in memory, the file named by METALBLAS_PLAN_CACHE
+    planner.clear()
+    dispatch._DESC_CACHE.clear()
+    timed = []
+    monkeypatch.setattr(planner, "_autotune", lambda *a, **k: timed.append(1))
+    for (tag, call, _), want in zip(cases, first):
+        got = call()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"{tag}: the cached plan gave different bits"
+    assert not timed, "a plan in the cache file was tuned again"
+    assert planner.cached() == {k: (tuple(v) if v is not None else None) for k, v in on_disk.items()}
+    planner.clear()
+    dispatch._DESC_CACHE.clear()
+
+
+def test_tuner_off_keeps_static_plans(dev, monkeypatch):
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "0")
+    monkeypatch.delenv("METALBLAS_PLAN_CACHE", raising=False)
+    planner.clear()
+    dispatch._DESC_CACHE.clear()
+    called = []
+    monkeypatch.setattr(planner, "_autotune", lambda *a, **k: called.append(1))
+    g = gen(22)
+    a = torch.randn(2048, 4096, generator=g).to(torch.bfloat16)
+    b = torch.randn(4096, 2048, generator=g).to(torch.bfloat16)
+    got = mb.matmul(a.to(dev), b.to(dev))
+    assert_parity(got, a, b, tag="static plan")
+    assert not called and not planner.cached()
+    dispatch._DESC_CACHE.clear()
+
+
+def test_import_name_is_the_references(dev):
+    """``import metalblas`` (the reference's package name, pyproject.toml:6) runs this library."""
+    import metalblas
+    from metalblas.kernels import has_metal4
+    assert has_metal4()
+    assert metalblas.matmul is mb.matmul and metalblas.bmm is mb.bmm
+    g = gen(23)
+    a, b = rand((300, 200), torch.bfloat16, g), rand((200, 100), torch.bfloat16, g)
+    assert_parity(metalblas.matmul(a.to(dev), b.to(dev)), a, b, tag="import metalblas")
+
+
+@pytest.mark.parametrize("swz", [0, 1, 2, 3, 5, 6])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=str)
+def test_swizzle_log(dev, swz, dtype):
+    """``swizzle_log=`` only reorders the tiles (float_dispatch.py:711-717): every value gives
+    the same product."""
+    g = gen(24 + swz)
+    M, N, K = 1100, 1300, 512
+    a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
+    got = mb.matmul(a.to(dev), b.to(dev), backend="mpp_tensor", swizzle_log=swz)
+    assert_parity(got, a, b, tag=f"swizzle_log={swz} {dtype}")

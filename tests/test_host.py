@@ -117,8 +117,12 @@ def test_abi_rejects_bad_descriptors_before_launch():
     d.backend = 17
     assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_BAD_BACKEND
     d = _desc(torch.float32, a, a)
-    d.flags = 1
+    d.flags = 2                      # an unknown flag bit
     assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    # a dry run plans and returns without queuing work (host pointers never reach a kernel)
+    d = _desc(torch.float32, a, a)
+    d.flags = _lib.FLAG_DRY_RUN
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.OK
     d = _desc(torch.float32, a, a)
     d.M = -1
     assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
@@ -303,6 +307,22 @@ def test_tile_candidates_primary_first():
 
 # ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
 
+@pytest.mark.parametrize("dt", [torch.int8, torch.uint8, torch.bfloat16, torch.float16, torch.float32], ids=str)
+def test_tile_candidates_are_compiled_tiles(dt):
+    """Every autotune candidate names a tile compiled for the dtype: the 8-bit ping-pong
+    schedule exists at 256 x 256 only (a 256 x 128 ping-pong candidate cannot launch)."""
+    a = torch.empty(4096, 4096, dtype=dt)
+    cands = _lib.tile_candidates(_desc(dt, a, a))
+    assert len(cands) > 1
+    for t in cands:
+        if dt in (torch.int8, torch.uint8) and t[5] == 2:
+            assert t[:2] == (256, 256), t
+    # a forced 256 x 128 ping-pong tile snaps to a compiled 8-bit tile
+    if dt in (torch.int8, torch.uint8):
+        info = _plan(dt, a, a, backend=_lib.BACKEND_TILED, tile=(256, 128, 128, 2, 4, 2))
+        assert not (info.tile[5] == 2 and info.tile[1] != 256), tuple(info.tile)
+
+
 def test_unit_lead_classification():
     """metalblas/dispatch.py:23-35 on the BASELINE config-3 layouts."""
     M, K = 64, 96
@@ -367,12 +387,24 @@ def test_api_surface_matches_reference():
         assert bk in dispatch.BACKENDS
 
 
+def test_import_name_matches_reference():
+    """``import metalblas`` (the reference's package name, /root/reference/pyproject.toml:6) exports
+    the reference's names (metalblas/__init__.py:1-19), bound to this library."""
+    import metalblas
+    from metalblas.kernels import has_metal4
+    assert sorted(metalblas.__all__) == sorted(mb.__all__)
+    for name in metalblas.__all__:
+        if name != "kernels":
+            assert getattr(metalblas, name) is getattr(mb, name), name
+    assert has_metal4 is mb.kernels.has_metal4
+
+
 def test_autotune_probe_params_and_cache(tmp_path, monkeypatch):
     w0 = planner.probe_params(256, 256, 256)
     w2 = planner.probe_params(8192, 8192, 8192)
     assert w0[1] >= w2[1] and w0[0] >= w2[0]
     path = tmp_path / "plans.json"
-    monkeypatch.setattr(planner, "_CACHE_PATH", str(path))
+    monkeypatch.setenv("METALBLAS_PLAN_CACHE", str(path))
     planner.clear()
     planner._PLANS["k1"] = (256, 256, 64, 2, 4, 0, 0, 0)
     planner._PLANS["k2"] = None
@@ -380,20 +412,39 @@ def test_autotune_probe_params_and_cache(tmp_path, monkeypatch):
     saved = json.loads(path.read_text())
     assert saved["k1"][:2] == [256, 256] and saved["k2"] is None
     planner.clear()
-    monkeypatch.setattr(planner, "_loaded", False)
     planner._load_cache()
-    assert planner.cached()["k1"][:2] == (256, 256)
+    assert planner.cached()["k1"][:2] == (256, 256) and planner.cached()["k2"] is None
+    # a second file is merged in when the variable names it; plans already held win
+    other = tmp_path / "other.json"
+    other.write_text(json.dumps({"k1": [64, 64, 64, 2, 2, 0, 0, 0], "k3": [128, 128, 64, 2, 2, 0, 0, 0]}))
+    monkeypatch.setenv("METALBLAS_PLAN_CACHE", str(other))
+    planner._load_cache()
+    assert planner.cached()["k1"][:2] == (256, 256) and planner.cached()["k3"][:2] == (128, 128)
     planner.clear()
 
 
 def test_autotune_switch(monkeypatch):
-    """Opt-in: only METALBLAS_AUTOTUNE=1 enables the tuner."""
+    """As the reference (metalblas/float_dispatch.py:156): on unless METALBLAS_AUTOTUNE=0."""
     monkeypatch.delenv("METALBLAS_AUTOTUNE", raising=False)
-    assert not planner.enabled()
+    assert planner.enabled()
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "0")
     assert not planner.enabled()
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
     assert planner.enabled()
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "yes")
+    assert planner.enabled()
+
+
+def test_tuner_scratch_keeps_output_layout():
+    """Candidates are timed into scratch with the real output's strides and pointer alignment."""
+    base = torch.empty(40 * 33 + 17, dtype=torch.bfloat16)
+    out = base[17:].as_strided((33, 40), (1, 33))          # column-major at a 34-byte offset
+    s = planner._like_out(out)
+    assert s.shape == out.shape and s.stride() == out.stride()
+    assert s.data_ptr() % 256 == out.data_ptr() % 256
+    out3 = torch.empty(3, 64, 48, dtype=torch.complex64)[:, :, ::1]
+    s3 = planner._like_out(out3)
+    assert s3.stride() == out3.stride() and s3.data_ptr() % 256 == out3.data_ptr() % 256
 
 
 def test_product_never_touches_the_oracle():

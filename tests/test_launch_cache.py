@@ -4,8 +4,9 @@ mb_gemm plans a call signature once on sentinel pointers and relocates the cache
 fields to each later call's operands.  With METALBLAS_LAUNCH_CACHE=verify the library also replans
 every cache hit from the real descriptor and aborts when any relocated pointer or launch choice
 differs.  Here every plan family is driven through mb_gemm three times per signature, with the
-operands (and workspace) moved to new addresses between calls; without a GPU each call ends at
-the kernel launch (MB_ERR_LAUNCH), after planning, relocation and the verify comparison.
+operands (and workspace) moved to new addresses between calls.  Every call carries
+MB_FLAG_DRY_RUN: mb_gemm plans, relocates and verifies, then returns MB_OK without queuing any
+work, so the made-up pointers never reach a kernel, with or without a GPU in the machine.
 """
 from __future__ import annotations
 
@@ -35,12 +36,12 @@ def run(name, dt, batch, M, N, K, a, b, c, bias=None, low=0, ws=True, **kw):
         base = 0x7f0000000000 + shift
         ops = [None if m is None else (Ptr(base + i * (1 << 40) + low * (i + 1)),) + tuple(m)
                for i, m in enumerate((a, b, c, bias))]
-        d = _lib.make_desc(dt, batch, M, N, K, *ops, **kw)
+        d = _lib.make_desc(dt, batch, M, N, K, *ops, flags=_lib.FLAG_DRY_RUN, **kw)
         need = _lib.workspace_bytes(d)
         if need and ws:
             d.workspace, d.workspace_bytes = 0x7e0000000000 + shift, need
         codes.add(lib.mb_gemm(ctypes.byref(d), None))
-    assert codes <= {_lib.ERR_LAUNCH, _lib.OK}, (name, codes)
+    assert codes == {_lib.OK}, (name, codes)
     print("ok", name, flush=True)
 
 bf, f16, f32 = torch.bfloat16, torch.float16, torch.float32
