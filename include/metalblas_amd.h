@@ -72,7 +72,9 @@ typedef enum mb_status {
     MB_ERR_LAUNCH = -5,             /* hipGetLastError() after a launch */
     MB_ERR_NO_DEVICE = -6,
     MB_ERR_GEMV_SHAPE = -7,         /* backend GEMV with M != 1 and N != 1 */
-    MB_ERR_BAD_BACKEND = -8
+    MB_ERR_BAD_BACKEND = -8,
+    MB_ERR_SCRATCH_LIMIT = -9       /* mb_gemm_noalloc: the product needs more scratch than its
+                                       static buffer holds */
 } mb_status;
 
 /* A strided (batched) matrix operand.  Element (b, r, c) lives at
@@ -145,6 +147,22 @@ typedef enum mb_family {
  * METALBLAS_LAUNCH_CACHE=0 disables the cache; =verify replans every hit and aborts on a
  * difference. */
 int mb_gemm(const mb_gemm_desc *desc, void *stream);
+
+/* mb_gemm() without a workspace and without any allocation.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The split-K planes, operand copies and complex
+ * expansions a product needs run in a static per-device buffer of
+ * mb_gemm_noalloc_scratch_bytes() bytes (64 MiB, enough for every BASELINE workload) that the
+ * library holds on each device it runs on until the process ends; desc->workspace and
+ * desc->workspace_bytes are ignored.  The same plan and kernels as mb_gemm() with a workspace
+ * run, so results are identical.  A product that needs more scratch than the buffer holds
+ * returns MB_ERR_SCRATCH_LIMIT and queues nothing.  Calls share the device's buffer: calls that
+ * overlap on one device (different streams or host threads) race; calls queued on one stream
+ * are ordered and safe.  desc->flags may be 0 or MB_FLAG_DRY_RUN. */
+int mb_gemm_noalloc(const mb_gemm_desc *desc, void *stream);
+
+/* Size of mb_gemm_noalloc's static per-device scratch buffer, in bytes. */
+int64_t mb_gemm_noalloc_scratch_bytes(void);
 
 /* Bytes of device scratch mb_gemm() needs for this descriptor (0 if none); negative on error.
  * Replaces the pooled split-K partial planes of metalblas/float_dispatch.py:183-192. */

@@ -49,6 +49,7 @@ ERR_LAUNCH = -5
 ERR_NO_DEVICE = -6
 ERR_GEMV_SHAPE = -7
 ERR_BAD_BACKEND = -8
+ERR_SCRATCH_LIMIT = -9
 
 # mb_gemm_desc.flags bits
 FLAG_DRY_RUN = 1
@@ -58,8 +59,9 @@ QUERY_ABI_VERSION, QUERY_HAS_MATRIX_CORES, QUERY_CU_COUNT, QUERY_GFX_ARCH, QUERY
 
 ABI_VERSION = 1
 
-EXPORTED_SYMBOLS = ("mb_gemm", "mb_gemm_workspace_bytes", "mb_plan", "mb_tile_candidates",
-                    "mb_query", "mb_strerror")
+EXPORTED_SYMBOLS = ("mb_gemm", "mb_gemm_noalloc", "mb_gemm_noalloc_scratch_bytes",
+                    "mb_gemm_workspace_bytes", "mb_plan", "mb_tile_candidates", "mb_query",
+                    "mb_strerror")
 
 
 class MbMatrix(ctypes.Structure):
@@ -108,6 +110,10 @@ def load(path: str = LIB_PATH):
     lib = ctypes.CDLL(path)
     lib.mb_gemm.argtypes = [ctypes.POINTER(MbGemmDesc), ctypes.c_void_p]
     lib.mb_gemm.restype = ctypes.c_int
+    lib.mb_gemm_noalloc.argtypes = [ctypes.POINTER(MbGemmDesc), ctypes.c_void_p]
+    lib.mb_gemm_noalloc.restype = ctypes.c_int
+    lib.mb_gemm_noalloc_scratch_bytes.argtypes = []
+    lib.mb_gemm_noalloc_scratch_bytes.restype = ctypes.c_int64
     lib.mb_gemm_workspace_bytes.argtypes = [ctypes.POINTER(MbGemmDesc)]
     lib.mb_gemm_workspace_bytes.restype = ctypes.c_int64
     lib.mb_plan.argtypes = [ctypes.POINTER(MbGemmDesc), ctypes.POINTER(MbPlanInfo)]

@@ -22,6 +22,10 @@
 
 using namespace mb;
 
+// Scratch of the allocation-free entry point mb_gemm_noalloc (see scratch_address below).
+static constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
 namespace {
 
 constexpr int64_t kI32Max = 2147483647;
@@ -118,13 +122,18 @@ int ilog2_floor(int64_t v) {
     return r;
 }
 
+// Internal descriptor flag (never accepted from a caller): the call runs on the static scratch
+// of mb_gemm_noalloc, so a plan that needs more scratch than it holds is an error rather than a
+// fall-back to the plan without scratch.
+constexpr int32_t kFlagStaticScratch = 1 << 30;
+
 int normalise(const mb_gemm_desc *d, Prob &p) {
     if (!d) return MB_ERR_INVALID_ARG;
     if (d->dtype < 0 || d->dtype >= MB_DTYPE_COUNT) return MB_ERR_UNSUPPORTED_DTYPE;
     if (d->backend < 0 || d->backend >= MB_BACKEND_COUNT) return MB_ERR_BAD_BACKEND;
     if (d->batch < 0 || d->M < 0 || d->N < 0 || d->K < 0) return MB_ERR_INVALID_ARG;
     if (d->batch > kI32Max || d->M > kI32Max || d->N > kI32Max || d->K > kI32Max) return MB_ERR_INVALID_ARG;
-    if (d->flags & ~MB_FLAG_DRY_RUN) return MB_ERR_INVALID_ARG;
+    if (d->flags & ~(MB_FLAG_DRY_RUN | kFlagStaticScratch)) return MB_ERR_INVALID_ARG;
     p.dt = d->dtype;
     p.batch = d->batch;
     p.M = d->M;
@@ -967,6 +976,7 @@ int plan_one(const mb_gemm_desc *desc, Plan &pl) {
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
     if (pl.ws_bytes > 0 && (!desc->workspace || desc->workspace_bytes < pl.ws_bytes)) {
+        if (desc->flags & kFlagStaticScratch) return MB_ERR_SCRATCH_LIMIT;
         pl = Plan();
         st = make_plan(desc, pl, false);
     }
@@ -1178,12 +1188,64 @@ int cached_plan(const mb_gemm_desc *desc, CallPlan &cp) {
     return MB_OK;
 }
 
+// ---- allocation-free entry point -----------------------------------------------------------
+// mb_gemm_noalloc runs on this file-scope device array instead of a caller's workspace.  Each
+// device that loads the library holds its own copy (64 MiB) until the process ends.  In host
+// code `scratch` is only a host-side stand-in for the symbol: its device address on the current
+// device comes from hipGetSymbolAddress, taken once per device on the first call there and kept
+// in g_scratch_ptr; only that address is ever handed to a kernel.  No byte of it needs to start
+// at zero: every scratch byte a kernel reads (split-K partial planes, operand copies, the complex
+// expansion) was written earlier in the same call.  Calls that overlap on one device (other
+// streams, other host threads) share the array and race.
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64];
+
+int scratch_address(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return MB_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) return MB_ERR_NO_DEVICE;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MB_OK;
+}
+
+int gemm_impl(const mb_gemm_desc *desc, void *stream);
+
 }  // namespace
 
 extern "C" {
 
 int mb_gemm(const mb_gemm_desc *desc, void *stream) {
     if (!desc) return MB_ERR_INVALID_ARG;
+    if (desc->flags & kFlagStaticScratch) return MB_ERR_INVALID_ARG;
+    return gemm_impl(desc, stream);
+}
+
+int mb_gemm_noalloc(const mb_gemm_desc *desc, void *stream) {
+    if (!desc) return MB_ERR_INVALID_ARG;
+    if (desc->flags & ~MB_FLAG_DRY_RUN) return MB_ERR_INVALID_ARG;
+    mb_gemm_desc d = *desc;
+    void *p = nullptr;
+    const int st = scratch_address(&p);
+    if (st != MB_OK) return st;
+    d.workspace = p;
+    d.workspace_bytes = kScratchBytes;
+    d.flags |= kFlagStaticScratch;
+    return gemm_impl(&d, stream);
+}
+
+int64_t mb_gemm_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+}  // extern "C"
+
+namespace {
+
+int gemm_impl(const mb_gemm_desc *desc, void *stream) {
     CallPlan cp;
     const int st = cache_mode() ? cached_plan(desc, cp) : plan_call(desc, cp);
     if (st != MB_OK) return st;
@@ -1196,6 +1258,10 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream) {
     }
     return MB_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
     Peel pe;
@@ -1313,6 +1379,9 @@ const char *mb_strerror(int32_t status) {
         case MB_ERR_NO_DEVICE: return "no HIP device";
         case MB_ERR_GEMV_SHAPE: return "gemv backend requires M==1 or N==1";
         case MB_ERR_BAD_BACKEND: return "unknown backend";
+        case MB_ERR_SCRATCH_LIMIT:
+            return "the product needs more scratch than mb_gemm_noalloc's static buffer holds "
+                   "(mb_gemm_noalloc_scratch_bytes()); call mb_gemm with a workspace instead";
     }
     return "unknown status";
 }
