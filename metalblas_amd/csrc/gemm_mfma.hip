@@ -23,6 +23,7 @@ hipError_t launch_i8_kwhole(const MfmaTile &, bool, bool, const GemmArgs &, dim3
 hipError_t launch_i8_ktail(const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_i8_pp(bool ktail, bool, bool, const GemmArgs &, dim3, hipStream_t);
 hipError_t launch_thin(int dt, bool ktail, const MfmaTile &, bool, bool, const GemmArgs &, dim3, hipStream_t);
+hipError_t launch_deepk(int dt, bool ktail, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st);
 }  // namespace m16
 
 namespace {
@@ -44,6 +45,8 @@ constexpr TileEntry kTiles16[] = {
     // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 (A K-contiguous, B
     // N-contiguous)
     {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},  {4, 16, 1, 1, 0},
+    // the deep-K schedule of the 64 x 64 tile (bf16 / fp16): few output tiles, many K slices
+    {64, 64, 2, 2, 2},
 };
 
 // dtypes of the LDS-direct family
@@ -75,6 +78,7 @@ int mfma_k_align(int dt) { return 16 / dtype_size(dt); }
 
 bool mfma_tile_compiled(int dt, const MfmaTile &t) {
     if ((dt == I8 || dt == U8) && t.sched == 1 && t.bn != 256) return false;   // 8-bit ping-pong: 256 x 256 only
+    if (t.sched == 2 && dt != BF16 && dt != F16) return false;                  // deep-K: 16-bit floats only
     if (is16(dt)) return in_table(kTiles16, sizeof(kTiles16) / sizeof(kTiles16[0]), t);
     return in_table(kTiles, sizeof(kTiles) / sizeof(kTiles[0]), t);
 }
@@ -103,6 +107,11 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
             const bool whole = (g.k_chunk % bk) == 0 && (g.K % bk) == 0;
             if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256) || (t.bm == 4 && t.bn == 16))
                 return m16::launch_thin(dt, !whole, t, a_kc, b_kc, g, grid, st);
+            if (t.sched == 2) {   // deep-K: a 1-D grid of (K slice, tile) workgroups
+                const dim3 g1(tiles * g.splits, 1, grid.z);
+                if (shape) *shape = {g1, dim3(256)};
+                return m16::launch_deepk(dt, !whole, a_kc, b_kc, g, g1, st);
+            }
             if (t.sched == 1) {
                 if (dt == BF16) return m16::launch_bf16_pp(!whole, t.bn, a_kc, b_kc, g, grid, st);
                 if (dt == F16) return m16::launch_f16_pp(!whole, t.bn, a_kc, b_kc, g, grid, st);

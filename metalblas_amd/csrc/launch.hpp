@@ -140,7 +140,8 @@ hipError_t launch_gemv_axpy_fast(int dt, const GemvArgs &g, hipStream_t st, Laun
 // gemm_mfma.hip
 struct MfmaTile {
     int bm, bn, wm, wn;   // block tile and wave grid
-    int sched = 0;        // 0: interleaved LDS reads / MFMAs per wave; 1: two-group ping-pong
+    int sched = 0;        // 0: interleaved LDS reads / MFMAs per wave; 1: two-group ping-pong;
+                          // 2: deep-K streaming ring over a 1-D grid of K slices (64 x 64, bf16 / fp16)
 };
 bool mfma_supported_dtype(int dt);
 int mfma_k_align(int dt);   // elements per 16-byte chunk along K

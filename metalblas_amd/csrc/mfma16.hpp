@@ -647,7 +647,23 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 // 2 MFMAs per 16-deep k-step per wave; they are not the limit.
 template <int N> __device__ __forceinline__ void vm_wait_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
-template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL, int NST>
+// Output tile and K slice of workgroup `pid` of a 1-D grid of n = tiles x splits workgroups:
+// workgroup i runs on XCD i % 8, and the workgroups of one XCD take consecutive (slice, tile)
+// indices, so the tiles of a K slice, which read the same slabs of A and B, share one XCD's L2
+// (the remap is a bijection on [0, n) for any n).
+__device__ __forceinline__ void slice_coords(int pid, int n, int tiles, int &tile, int &ks) {
+    if (n >= 16) {
+        const int xcd = pid & 7, idx = pid >> 3;
+        const int base = n >> 3, rem = n & 7;
+        pid = xcd * base + min(xcd, rem) + idx;
+    }
+    tile = pid % tiles;
+    ks = pid / tiles;
+}
+
+// XMAP: one workgroup per (tile, K slice) on a 1-D grid in slice_coords order (deep-K products:
+// few output tiles, many K slices); otherwise blockIdx.x is the tile and blockIdx.y the slice.
+template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL, int NST, bool XMAP = false>
 __global__ __launch_bounds__(64 * WM * WN) void k_thin16(GemmArgs g) {
     constexpr int NW = WM * WN;
     constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -669,10 +685,17 @@ __global__ __launch_bounds__(64 * WM * WN) void k_thin16(GemmArgs g) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave % WM, wn = wave / WM;
     const int tiles_m = cdiv(g.M, BM), tiles_n = cdiv(g.N, BN);
-    int tm, tn;
-    tile_coords16(blockIdx.x, tiles_m, tiles_n, g.swz, tm, tn);
+    int tm, tn, ks;
+    if constexpr (XMAP) {
+        int tile;
+        slice_coords(blockIdx.x, gridDim.x, tiles_m * tiles_n, tile, ks);
+        tm = tile % tiles_m;
+        tn = tile / tiles_m;
+    } else {
+        tile_coords16(blockIdx.x, tiles_m, tiles_n, g.swz, tm, tn);
+        ks = blockIdx.y;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
-    const int ks = blockIdx.y;
     const int kbeg = ks * g.k_chunk;
     const int kend = min(g.K, kbeg + g.k_chunk);
     const int klen = kend - kbeg;
@@ -764,6 +787,23 @@ hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs
     if (!(t.bm == 32 && t.bn == 256 && t.wm == 1 && t.wn == 4 && a_kc && !b_kc)) return hipErrorInvalidValue;
     hipLaunchKernelGGL((k_thin16<T, 32, 256, 1, 4, true, false, KTAIL, 4>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
+}
+
+// The deep-K schedule (sched 2) of the 64 x 64 tile: products with few output tiles and a deep
+// K, split into K slices so that ~256 workgroups stream the operands through a 4-deep ring of
+// 16 KiB LDS-direct stages; the tiles of a slice run on one XCD (slice_coords), so each slab
+// of A and B comes from HBM once.  Measured on MI355X for fp16 128 x 128 x 65536 (64 slices):
+// 7.7 us against 11.6 us for the 2-D grid (tiles of a slice on different XCDs) and 14.4 us
+// for the two-buffer 64 x 128 tile; deeper rings (5..8 stages) measured 8.5-9.4 us.
+template <class T, bool A_KC, bool B_KC, bool KTAIL>
+hipError_t launch_deepk16_t(const GemmArgs &g, dim3 grid, hipStream_t st) {
+    hipLaunchKernelGGL((k_thin16<T, 64, 64, 2, 2, A_KC, B_KC, KTAIL, 4, true>), grid, dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+template <class T, bool KTAIL>
+hipError_t launch_deepk16(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    if (a_kc) return b_kc ? launch_deepk16_t<T, true, true, KTAIL>(g, grid, st) : launch_deepk16_t<T, true, false, KTAIL>(g, grid, st);
+    return b_kc ? launch_deepk16_t<T, false, true, KTAIL>(g, grid, st) : launch_deepk16_t<T, false, false, KTAIL>(g, grid, st);
 }
 
 // Ping-pong schedule of the 256 x 256 tile with 8 waves, two per SIMD (waves w and w + 4

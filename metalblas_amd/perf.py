@@ -9,9 +9,15 @@ this GPU instead of wall clocks around ``torch.mps.synchronize``.
     python -m metalblas_amd.perf --group square --dtype fp16
     python -m metalblas_amd.perf --layout all --check    # layout sweep with a parity check
     python -m metalblas_amd.perf --report                # write profiles/shape_sweep_<gpu>.md
+    python -m metalblas_amd.perf --bmm --check           # the bmm groups (bench/bench_bmm.py)
+    python -m metalblas_amd.perf --trace-summary run_kernel_trace.csv --last 20
 
 Numbers are best-of-``trials`` means over ``iters`` back-to-back calls, so a
 power-limited product reports its sustained rate, not its first call.
+
+``--trace-summary`` reads a ``rocprofv3 --kernel-trace --output-format csv`` trace and prints
+per-kernel dispatch statistics as a Markdown table; ``--last N`` keeps only each kernel's last N
+dispatches (the timed steps of a benchmark whose planning and warmup calls come first).
 """
 from __future__ import annotations
 
@@ -35,6 +41,16 @@ SHAPES = {
     "thin_n": [(4096, 128, 4096), (4096, 256, 4096), (8192, 128, 4096), (4096, 64, 4096), (4096, 32, 4096),
                (4096, 16, 4096), (4096, 8, 4096)],
     "odd": [(257, 257, 257), (1023, 1023, 1023), (4097, 4097, 4097), (511, 511, 511), (333, 444, 555)],
+}
+
+# the reference's bmm shape groups, (B, M, N, K) (bench/bench_bmm.py:51-63)
+BMM_SHAPES = {
+    "attn": [(96, 512, 512, 64), (96, 512, 64, 512), (192, 512, 512, 64), (192, 512, 64, 512),
+             (32, 1024, 1024, 128), (32, 1024, 128, 1024), (48, 2048, 2048, 64)],
+    "square": [(64, 128, 128, 128), (64, 256, 256, 256), (32, 512, 512, 512),
+               (16, 1024, 1024, 1024), (8, 256, 256, 256), (256, 128, 128, 128)],
+    "thin": [(128, 64, 4096, 256), (128, 4096, 64, 256), (256, 32, 2048, 512), (64, 16, 4096, 512)],
+    "small": [(512, 64, 64, 64), (1024, 32, 32, 64), (2048, 64, 64, 32)],
 }
 
 DTYPES = {
@@ -139,6 +155,65 @@ def bench_one(M, N, K, dtype, build_a=_rm, build_b=_rm, check=False, cool=0.0):
     return flops, t_torch, t_mb, ok
 
 
+def _ok_bmm(a, b, dtype):
+    """Sampled batches of a bmm against a CPU float64 product (the bar of _ok)."""
+    idx = sorted({0, a.shape[0] // 2, a.shape[0] - 1})
+    got = _mb.bmm(a, b)[idx].cpu().double()
+    ref = torch.bmm(a[idx].cpu().double(), b[idx].cpu().double())
+    tol = 2e-2 if dtype in (torch.float16, torch.bfloat16) else 1e-3
+    return (got - ref).abs().max().item() <= tol * (ref.abs().max().item() or 1.0)
+
+
+def bench_bmm_one(B, M, N, K, dtype, check=False):
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = torch.randn(B, M, K, generator=g, device="cuda", dtype=dtype)
+    b = torch.randn(B, K, N, generator=g, device="cuda", dtype=dtype)
+    flops = 2.0 * B * M * N * K
+    iters = _plan_iters(flops)
+    t_torch = _time(lambda: torch.bmm(a, b), iters, 5, 3)
+    t_mb = _time(lambda: _mb.bmm(a, b), iters, 5, 3)
+    ok = _ok_bmm(a, b, dtype) if check else None
+    return flops, t_torch, t_mb, ok
+
+
+def run_bmm_group(name, shapes, dtype, check=False, out=print):
+    out(f"\n=== bmm {name}  dtype={str(dtype).replace('torch.', '')} ===")
+    out(f"{'B':>4} " + HEADER + ("  chk" if check else ""))
+    speedups = []
+    for (B, M, N, K) in shapes:
+        try:
+            flops, tt, tm, ok = bench_bmm_one(B, M, N, K, dtype, check)
+            out(_fmt(M, N, K, flops, tt, tm, ok, prefix=f"{B:>4} "))
+            speedups.append(tt / tm)
+        except Exception as ex:
+            out(f"{B:>4} {M:>5} {N:>5} {K:>5} | FAILED: {type(ex).__name__}: {ex}")
+    if speedups:
+        out(f"median speedup {statistics.median(speedups):.2f}x  (min {min(speedups):.2f}x, max {max(speedups):.2f}x)")
+    return speedups
+
+
+def trace_summary(path, last=0, names=None):
+    """Markdown table of a rocprofv3 kernel trace (CSV): calls, average / min / max duration per
+    kernel, over each kernel's last ``last`` dispatches when last > 0."""
+    import csv
+    durs = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row.get("Kernel_Name") or row.get("KernelName") or row.get("Name")
+            t0 = int(row.get("Start_Timestamp") or row.get("BeginNs"))
+            t1 = int(row.get("End_Timestamp") or row.get("EndNs"))
+            durs.setdefault(name, []).append((t0, t1 - t0))
+    lines = ["| kernel | calls | avg us | min us | max us |", "|---|---:|---:|---:|---:|"]
+    for name, v in sorted(durs.items(), key=lambda kv: -sum(d for _, d in kv[1])):
+        if names and not any(n in name for n in names):
+            continue
+        v.sort()
+        d = [x for _, x in (v[-last:] if last > 0 else v)]
+        lines.append(f"| `{name[:150]}` | {len(d)} | {sum(d) / len(d) / 1e3:.2f} | {min(d) / 1e3:.2f} | "
+                     f"{max(d) / 1e3:.2f} |")
+    return "\n".join(lines)
+
+
 def _fmt(M, N, K, flops, t_torch, t_mb, ok, prefix=""):
     tt = f"{t_torch * 1e3:>9.3f} {flops / t_torch / 1e12:>7.2f}" if t_torch else f"{'-':>9} {'-':>7}"
     sp = f"{t_torch / t_mb:>5.2f}x" if t_torch else f"{'-':>6}"
@@ -198,6 +273,14 @@ def write_report(path, dtype=torch.bfloat16, layouts=None, check=False, cool=0.0
             "`torch` is `torch.matmul` (hipBLASLt / rocBLAS)",
             f"- median speedup over all shapes: {statistics.median(all_sp):.2f}x" if all_sp else "", "",
             f"## {str(dtype).replace('torch.', '')} results vs `torch.matmul`", "", "```", "\n\n".join(blocks), "```", ""]
+    bmm_blocks, bmm_sp = [], []
+    for g, shapes in BMM_SHAPES.items():
+        lines = []
+        bmm_sp += run_bmm_group(g, shapes, dtype, check=check, out=lines.append)
+        bmm_blocks.append("\n".join(lines))
+    text += [f"## bmm vs `torch.bmm` (the reference's bench/bench_bmm.py groups)", "",
+             f"- median speedup: {statistics.median(bmm_sp):.2f}x" if bmm_sp else "", "", "```",
+             "\n\n".join(bmm_blocks), "```", ""]
     if lay_blocks:
         text += ["## Layout sweep (rm = row-major, cm = column-major view, sliced = `[::2]` rows, "
                  "colsl = `[:, ::2]`, offset = `[1:, 1:]`)", "", "```", "\n\n".join(lay_blocks), "```", ""]
@@ -209,12 +292,19 @@ def write_report(path, dtype=torch.bfloat16, layouts=None, check=False, cool=0.0
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--dtype", default="bf16", choices=list(DTYPES) + ["all"])
-    p.add_argument("--group", default="all", choices=list(SHAPES) + ["all"])
+    p.add_argument("--group", default="all", choices=list(SHAPES) + list(BMM_SHAPES) + ["all"])
     p.add_argument("--layout", default=None, help="comma list of " + ",".join(LAYOUTS) + " or 'all'")
     p.add_argument("--check", action="store_true", help="compare every result with a CPU fp64/int64 product")
     p.add_argument("--cool", type=float, default=0.0, help="sleep this ratio of each benchmark's time after it")
     p.add_argument("--report", action="store_true", help="write profiles/shape_sweep_<gpu>.md (bf16)")
+    p.add_argument("--bmm", action="store_true", help="the bmm shape groups instead of the matmul ones")
+    p.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel trace and exit")
+    p.add_argument("--last", type=int, default=0, help="with --trace-summary: each kernel's last N dispatches")
+    p.add_argument("--kernel", action="append", help="with --trace-summary: kernels whose name contains this")
     args = p.parse_args(argv)
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.last, args.kernel))
+        return
     layouts = None
     if args.layout:
         layouts = list(LAYOUTS) if args.layout == "all" else args.layout.split(",")
@@ -228,6 +318,12 @@ def main(argv=None):
         print("wrote", write_report(path, layouts=layouts, check=args.check, cool=args.cool))
         return
     dtypes = list(DTYPES.values()) if args.dtype == "all" else [DTYPES[args.dtype]]
+    if args.bmm:
+        groups = list(BMM_SHAPES) if args.group == "all" else [args.group]
+        for dt in dtypes:
+            for g in groups:
+                run_bmm_group(g, BMM_SHAPES[g], dt, check=args.check)
+        return
     groups = list(SHAPES) if args.group == "all" else [args.group]
     for dt in dtypes:
         for g in groups:

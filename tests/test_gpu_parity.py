@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import metalblas_amd as mb
-from helpers import ALL, COMPLEX, FLOATS, INTS, assert_parity, gen, rand
+from helpers import ALL, COMPLEX, FLOATS, INTS, assert_parity, assert_parity_full, gen, rand
 
 pytestmark = pytest.mark.gpu
 
@@ -445,7 +445,8 @@ def test_gemv_config2_sizes(dev, n):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.int8, torch.uint8], ids=str)
 @pytest.mark.parametrize("tile", [(256, 256, 64, 2, 4, 1), (256, 256, 64, 2, 4, 2), (256, 128, 64, 2, 4, 2),
-                                  (256, 256, 64, 2, 2, 1), (128, 128, 64, 2, 2, 1), (64, 64, 64, 2, 2, 1)], ids=str)
+                                  (256, 256, 64, 2, 2, 1), (128, 128, 64, 2, 2, 1), (64, 64, 64, 2, 2, 1),
+                                  (64, 64, 64, 2, 2, 3)], ids=str)
 @pytest.mark.parametrize("shape", [(256, 256, 64), (513, 257, 129), (1000, 700, 1000), (512, 768, 4160),
                                    (64, 64, 4096)], ids=str)
 @pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
@@ -664,3 +665,29 @@ def test_complex64_gemv_streaming(dev, shape, conj):
     out = torch.empty(M, dtype=torch.complex64, device=dev)
     mb.matmul(A, X, out=out)
     assert torch.equal(out.cpu(), got.cpu())
+
+
+# ---- deep-K products on the streaming 64 x 64 schedule (K slices on a 1-D grid) ------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("shape", [(128, 128, 65536), (100, 200, 20000), (256, 192, 16448), (2, 96, 128, 24576)],
+                         ids=str)
+@pytest.mark.parametrize("layout", ["rr", "rc", "cr", "cc"])
+def test_deep_k(dev, dtype, shape, layout):
+    """Deep-K products: ragged tile edges, a K that ends inside a stage, a batch; every operand
+    layout; the fused epilogue on the row-major case."""
+    Bb = shape[0] if len(shape) == 4 else None
+    M, N, K = shape[-3:]
+    g = gen(M + N + K)
+    lead = (Bb,) if Bb else ()
+    a = rand(lead + (M, K), dtype, g) if layout[0] == "r" else rand(lead + (K, M), dtype, g).transpose(-2, -1)
+    b = rand(lead + (K, N), dtype, g) if layout[1] == "r" else rand(lead + (N, K), dtype, g).transpose(-2, -1)
+    ad, bd = _to(a, dev), _to(b, dev)
+    p = mb.kernels.plan(ad, bd)
+    assert p["tile"][5] == 3 and p["split_k"] > 1, p
+    got = mb.bmm(ad, bd) if Bb else mb.matmul(ad, bd)
+    assert_parity_full(got, ad, bd, rows=8, tag=f"deep-K {dtype} {shape} {layout}")
+    if layout == "rr" and not Bb:
+        bias = rand((N,), dtype, g).to(dev)
+        got = mb.addmm(bias, ad, bd, beta=0.5, alpha=-2.0)
+        assert_parity_full(got, ad, bd, bias=bias, beta=0.5, alpha=-2.0, rows=8, tag=f"deep-K addmm {dtype} {shape}")

@@ -238,11 +238,34 @@ def test_plan_config4_splitk_and_batches():
     p = _plan(torch.float16, a, b)
     assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k > 1
     assert p.workspace_bytes == p.split_k * 128 * 128 * 4
+    # the deep-K schedule (tile[5] = schedule + 1 = 3) of the 64 x 64 tile: 4 tiles x 64 slices
+    # of 1024 on a 1-D grid of 256 workgroups
+    assert tuple(p.tile)[:2] == (64, 64) and p.tile[5] == 3 and p.split_k == 64
+    assert tuple(p.grid) == (256, 1, 1)
     a = torch.empty(8, 512, 256, dtype=torch.float16)
     b = torch.empty(8, 256, 512, dtype=torch.float16)
     assert _lib.FAMILY_NAMES[_plan(torch.float16, a, b).family] == "mfma"
     bb = torch.empty(256, 512, dtype=torch.float16).expand(8, 256, 512)   # stride-0 batch
     assert _lib.FAMILY_NAMES[_plan(torch.float16, a, bb).family] == "mfma"
+
+
+@pytest.mark.parametrize("shape", [(128, 128, 65536), (256, 256, 16384), (100, 200, 20000), (64, 64, 65536),
+                                   (512, 512, 8192)], ids=str)
+def test_plan_deep_k(shape):
+    """Deep-K products (at most 64 tiles of 64 x 64, K >= 8192) take the deep-K schedule with
+    K slices of >= 1024 and about one workgroup per CU; int8, shallow K, or more tiles do not."""
+    M, N, K = shape
+    a, b = torch.empty(M, K, dtype=torch.bfloat16), torch.empty(K, N, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, a, b)
+    tiles = -(-M // 64) * -(-N // 64)
+    assert p.tile[5] == 3 and tuple(p.tile)[:2] == (64, 64), tuple(p.tile)
+    assert 2 <= p.split_k <= 256 // tiles and -(-K // p.split_k) >= 1024 - 63
+    assert p.grid[0] == tiles * p.split_k and p.grid[1] == 1
+    assert len(_lib.tile_candidates(_desc(torch.bfloat16, a, b))) == 1
+    ai, bi = torch.empty(M, K, dtype=torch.int8), torch.empty(K, N, dtype=torch.int8)
+    assert _plan(torch.int8, ai, bi).tile[5] != 3
+    a2 = torch.empty(M, 4096, dtype=torch.bfloat16)
+    assert _plan(torch.bfloat16, a2, torch.empty(4096, N, dtype=torch.bfloat16)).tile[5] != 3
 
 
 def test_plan_config5_int8_and_complex():
@@ -456,3 +479,16 @@ def test_product_never_touches_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert "import oracle" not in text and "from oracle" not in text, f
                 assert "mb_oracle" not in text and "libmb_oracle" not in text, f
+
+
+def test_trace_summary_keeps_the_last_dispatches(tmp_path):
+    """perf.trace_summary: per-kernel statistics of a rocprofv3 CSV kernel trace, optionally over
+    each kernel's last N dispatches (the timed steps after planning and warmup calls)."""
+    from metalblas_amd import perf
+    f = tmp_path / "t_kernel_trace.csv"
+    f.write_text("Kernel_Name,Start_Timestamp,End_Timestamp\nk_a,100,1100\nk_a,2000,4000\n"
+                 "k_b,5000,5500\nk_a,6000,7000\n")
+    full = perf.trace_summary(str(f))
+    assert "| `k_a` | 3 | 1.33 | 1.00 | 2.00 |" in full and "| `k_b` | 1 | 0.50 |" in full
+    last = perf.trace_summary(str(f), last=2, names=["k_a"])
+    assert "| `k_a` | 2 | 1.50 | 1.00 | 2.00 |" in last and "k_b" not in last
