@@ -12,12 +12,13 @@ import concurrent.futures as _cf
 import os
 import shutil
 import subprocess
-import tempfile
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libmetalblas_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# object files of the last build (kept for the sanitizer test's link; not shipped)
+OBJ_DIR = os.path.join(PKG_DIR, "_build", "obj")
 ARCH = os.environ.get("METALBLAS_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -56,16 +57,16 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     hipcc = _hipcc()
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
-    with tempfile.TemporaryDirectory(prefix="mb_build_") as tmp:
-        objs = [os.path.join(tmp, os.path.basename(s) + ".o") for s in srcs]
-        with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-            list(ex.map(_compile, [(hipcc, s, o) for s, o in zip(srcs, objs)]))
-        out_tmp = LIB_PATH + ".tmp"
-        cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs]
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(f"link failed:\n{proc.stderr[-6000:]}")
-        os.replace(out_tmp, LIB_PATH)
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = [os.path.join(OBJ_DIR, os.path.basename(s) + ".o") for s in srcs]
+    with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_compile, [(hipcc, s, o) for s, o in zip(srcs, objs)]))
+    out_tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr[-6000:]}")
+    os.replace(out_tmp, LIB_PATH)
     if verbose:
         print(f"built {LIB_PATH}")
     return LIB_PATH

@@ -17,7 +17,8 @@ import os
 import torch
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG_DIR, "libmetalblas_hip.so")
+# METALBLAS_LIB names another build of the same library (e.g. a sanitizer build for host tests)
+LIB_PATH = os.environ.get("METALBLAS_LIB") or os.path.join(PKG_DIR, "libmetalblas_hip.so")
 
 # mb_dtype codes
 DTYPE_CODE = {
