@@ -42,21 +42,29 @@ def device_info() -> dict:
     }
 
 
-def plan(a, b, *, batch=None, backend=None, out_dtype=None) -> dict:
+def plan(a, b, *, batch=None, backend=None, out_dtype=None, out=None, tuned=False) -> dict:
     """The plan libmetalblas_hip.so would run for ``a @ b`` (2-D or 3-D tensors): kernel
-    family, tile, split-K and workspace.  For tests and reports."""
+    family, tile, split-K and workspace.  For tests and reports.  With ``tuned=True`` the tile
+    the one-shot autotuner already chose for this call signature (``out``'s layout included)
+    replaces the static one; nothing is timed here."""
+    from . import planner
     from .dispatch import BACKENDS, _mat
     dtype = a.dtype
     if a.dim() == 3:
         Bb, M, K = a.shape
         N = b.shape[2]
-        c = torch.empty(Bb, M, N, dtype=out_dtype or dtype, device=a.device)
+        c = out if out is not None else torch.empty(Bb, M, N, dtype=out_dtype or dtype, device=a.device)
     else:
         Bb = 1
         M, K = a.shape
         N = b.shape[1]
-        c = torch.empty(M, N, dtype=out_dtype or dtype, device=a.device)
+        c = out if out is not None else torch.empty(M, N, dtype=out_dtype or dtype, device=a.device)
     desc = _lib.make_desc(dtype, Bb, M, N, K, _mat(a), _mat(b), _mat(c), backend=BACKENDS[backend])
+    if tuned:
+        tile = planner.cached().get(planner._key(desc, c.device))
+        if tile is not None:
+            for i, v in enumerate(tile):
+                desc.tile[i] = int(v)
     info = _lib.plan(desc)
     return {
         "family": _lib.FAMILY_NAMES.get(info.family, str(info.family)),

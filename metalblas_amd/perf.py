@@ -214,6 +214,28 @@ def trace_summary(path, last=0, names=None):
     return "\n".join(lines)
 
 
+def pmc_summary(path, kernel, last=0):
+    """Per-counter averages of a rocprofv3 --pmc counter_collection CSV over the dispatches of the
+    kernels whose name contains ``kernel`` (each kernel's last ``last`` dispatches when last > 0):
+    {counter: mean value per dispatch}, plus the number of dispatches averaged under "dispatches"."""
+    import csv
+    per = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if kernel not in row["Kernel_Name"]:
+                continue
+            per.setdefault(int(row["Dispatch_Id"]), {})[row["Counter_Name"]] = float(row["Counter_Value"])
+    ids = sorted(per)
+    if last > 0:
+        ids = ids[-last:]
+    out = {}
+    for i in ids:
+        for c, v in per[i].items():
+            out[c] = out.get(c, 0.0) + v / len(ids)
+    out["dispatches"] = len(ids)
+    return out
+
+
 def _fmt(M, N, K, flops, t_torch, t_mb, ok, prefix=""):
     tt = f"{t_torch * 1e3:>9.3f} {flops / t_torch / 1e12:>7.2f}" if t_torch else f"{'-':>9} {'-':>7}"
     sp = f"{t_torch / t_mb:>5.2f}x" if t_torch else f"{'-':>6}"
@@ -300,8 +322,21 @@ def main(argv=None):
     p.add_argument("--bmm", action="store_true", help="the bmm shape groups instead of the matmul ones")
     p.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel trace and exit")
     p.add_argument("--last", type=int, default=0, help="with --trace-summary: each kernel's last N dispatches")
-    p.add_argument("--kernel", action="append", help="with --trace-summary: kernels whose name contains this")
+    p.add_argument("--kernel", action="append", help="with --trace-summary / --pmc-summary: kernels whose name contains this")
+    p.add_argument("--pmc-summary", metavar="CSV", nargs="+",
+                   help="average rocprofv3 --pmc counter_collection CSVs per dispatch (of --kernel) and exit")
     args = p.parse_args(argv)
+    if args.pmc_summary:
+        kern = (args.kernel or [""])[0]
+        merged = {}
+        for path in args.pmc_summary:
+            for c, v in pmc_summary(path, kern, args.last).items():
+                if c != "dispatches":
+                    merged[c] = v
+        print("| counter | mean per dispatch |\n|---|---:|")
+        for c in sorted(merged):
+            print(f"| `{c}` | {merged[c]:.6g} |")
+        return
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.last, args.kernel))
         return

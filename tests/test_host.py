@@ -492,3 +492,17 @@ def test_trace_summary_keeps_the_last_dispatches(tmp_path):
     assert "| `k_a` | 3 | 1.33 | 1.00 | 2.00 |" in full and "| `k_b` | 1 | 0.50 |" in full
     last = perf.trace_summary(str(f), last=2, names=["k_a"])
     assert "| `k_a` | 2 | 1.50 | 1.00 | 2.00 |" in last and "k_b" not in last
+
+
+def test_pmc_summary_averages_the_last_dispatches(tmp_path):
+    """perf.pmc_summary: per-counter means of a rocprofv3 --pmc CSV over a kernel's last N
+    dispatches."""
+    from metalblas_amd import perf
+    f = tmp_path / "p_counter_collection.csv"
+    rows = ["Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value"]
+    for d, (a, b) in enumerate([(10, 1), (20, 2), (30, 3)], start=1):
+        rows += [f"{d},k_gemm,SQ_A,{a}", f"{d},k_gemm,SQ_B,{b}", f"{d},other,SQ_A,999"]
+    f.write_text("\n".join(rows) + "\n")
+    s = perf.pmc_summary(str(f), "k_gemm", last=2)
+    assert s["dispatches"] == 2 and s["SQ_A"] == 25 and s["SQ_B"] == 2.5
+    assert perf.pmc_summary(str(f), "k_gemm")["SQ_A"] == 20
