@@ -322,7 +322,189 @@ __global__ __launch_bounds__(256) void k_thin_dot4(GemmArgs g) {
     }
 }
 
+// ---- k_dotx: up to 8 vectors against a K-contiguous matrix, the whole K in one workgroup ----
+// The k_thin_dot4 stream (4 rows x 256 bytes per load instruction, v_mfma_f32_4x4x4 with one
+// k chunk per 4-lane block) without K slices: wave w of the NW-wave workgroup owns k
+// [1024 w, 1024 w + 1024) and keeps that piece of the 8 vectors in registers (2 groups x 8
+// chunks), so no partial planes and no reduction launch are needed.  A workgroup walks a
+// group of 16 row quads; after each quad the 16 k-chunk blocks are summed across lanes (DPP
+// row rotations, then lanes 16 / 32 apart) and lanes 0..3 park the quad's 4 x 8 sums in LDS;
+// after the group the NW waves' sums are added in wave order (deterministic) and stored with
+// the epilogue.  The matrix is read with non-temporal loads (it is streamed once).
+//
+// Vectors: K-contiguous (XKC, vector n at n * b_cs + k), or the natural K x 8 row-major block
+// (element (k, n) at k * b_rs + n, 16-byte rows), which each wave transposes through its own
+// LDS region in 256-row phases.  Measured on MI355X, 16384^2 bf16 matrix x 8 vectors:
+// 85 us natural / 82 us K-contiguous (0.79 / 0.82 of 8 TB/s); 92 us with cached loads.
+// The host guarantees N <= 8, K % 8 == 0, K <= NW * 1024, batch <= 65535 and 31-bit offsets.
+constexpr int kDotxPH = 256;                   // natural vector rows per LDS transpose phase
+constexpr int kDotxPitch = 2 * kDotxPH + 64;   // bytes per vector row of a phase (conflict-free reads)
+
+__device__ __forceinline__ uint4 ld_buf_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);   // nt
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// sum over the 16 lanes l' with l' % 4 == l % 4 (the k-chunk blocks of a 4 x 4 MFMA result)
+__device__ __forceinline__ float sum_blocks(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xf, 0xf, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+template <class T, int NW, bool XKC>
+__global__ __launch_bounds__(64 * NW) void k_dotx(GemmArgs g) {
+    constexpr int U = kDotxU, G = 2, KW = kDotxKW, QG = kDotxQG;
+    constexpr int XB = XKC ? 16 : NW * 8 * kDotxPitch, RB = NW * QG * 32 * 4;
+    __shared__ __attribute__((aligned(16))) char lds[XB > RB ? XB : RB];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 3, b = lane >> 2;   // row / column index in the 4 x 4 block; block = k chunk
+    const int kw = w * KW;
+    const bool full = kw + KW <= g.K;
+    const int nquads = cdiv(g.M, 4);
+    const int bz = blockIdx.z;
+    const __amdgpu_buffer_rsrc_t ra = buf_rsrc((const T *)g.a + bz * g.a_bs);
+    const __amdgpu_buffer_rsrc_t rb = buf_rsrc((const T *)g.b + bz * g.b_bs);
+    // the matrix chunks of row quad rq: row 4 rq + i (clamped), k = kw + 128 u + 8 b
+    auto load_w = [&](int rq, uint4 (&dst)[U]) {
+        const int row = min(4 * rq + i, g.M - 1);
+        const uint32_t base = (uint32_t)(((int64_t)row * g.a_rs + kw + 8 * b) * sizeof(T));
+        if (full) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) dst[u] = ld_buf_nt(ra, base, 256 * u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) dst[u] = ld_buf_nt(ra, kw + 128 * u + 8 * b < g.K ? base : kOOB, 256 * u);
+        }
+    };
+    int grp = blockIdx.x;
+    uint4 wa[U];
+    if (grp * QG < nquads) load_w(grp * QG, wa);   // in flight while the vectors are loaded
+    // this lane's vector chunks: vector 4 q + i, k = kw + 128 u + 8 b
+    uint4 xr[G][U];
+    if constexpr (XKC) {
+#pragma unroll
+        for (int q = 0; q < G; ++q)
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int n = 4 * q + i, k = kw + 128 * u + 8 * b;
+                const uint32_t off = n < g.N && k < g.K ? (uint32_t)(((int64_t)n * g.b_cs + k) * sizeof(T)) : kOOB;
+                xr[q][u] = ld_buf(rb, off, 0);
+            }
+    } else {
+        // natural rows: lane l takes row pairs (2 l, 2 l + 1) and (2 l + 128, 2 l + 129) of a
+        // phase, packs each vector's two values into one dword and stores it at [n][k]; the
+        // next phase's rows are in flight meanwhile
+        char *my = lds + w * 8 * kDotxPitch;
+        constexpr int NPH = KW / kDotxPH;
+        uint4 r0[2][2], r1[2][2];
+        auto xload = [&](int ph, uint4 (&d0)[2], uint4 (&d1)[2]) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int k = kw + kDotxPH * ph + 2 * (lane + 64 * j);   // even: k + 1 < K iff k < K
+                const bool in = k < g.K;
+                d0[j] = ld_buf(rb, in ? (uint32_t)((int64_t)k * g.b_rs * sizeof(T)) : kOOB, 0);
+                d1[j] = ld_buf(rb, in ? (uint32_t)((int64_t)(k + 1) * g.b_rs * sizeof(T)) : kOOB, 0);
+            }
+        };
+        xload(0, r0[0], r1[0]);
+        xload(1, r0[1], r1[1]);
+#pragma unroll
+        for (int ph = 0; ph < NPH; ++ph) {
+            const int s = ph & 1;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t a0[4] = {r0[s][j].x, r0[s][j].y, r0[s][j].z, r0[s][j].w};
+                const uint32_t a1[4] = {r1[s][j].x, r1[s][j].y, r1[s][j].z, r1[s][j].w};
+#pragma unroll
+                for (int n = 0; n < 8; ++n) {
+                    const uint32_t lo = a0[n >> 1], hi = a1[n >> 1];
+                    const uint32_t v = (n & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+                    *(uint32_t *)(my + n * kDotxPitch + 4 * (lane + 64 * j)) = v;
+                }
+            }
+            if (ph + 2 < NPH) xload(ph + 2, r0[s], r1[s]);
+            __syncthreads();   // the region is the wave's own; the barrier orders its lanes' LDS writes and reads
+#pragma unroll
+            for (int up = 0; up < 2; ++up)
+#pragma unroll
+                for (int q = 0; q < G; ++q)
+                    xr[q][2 * ph + up] = *(const uint4 *)(my + (4 * q + i) * kDotxPitch + 256 * up + 16 * b);
+            __syncthreads();   // the next phase overwrites the region
+        }
+    }
+    float *red = (float *)lds;   // [wave][quad of the group][group q][column i][row r]
+    for (; grp * QG < nquads; grp += gridDim.x) {
+        const int q0 = grp * QG;
+        for (int t = 0; t < QG; ++t) {
+            f32x4 acc[G];
+#pragma unroll
+            for (int q = 0; q < G; ++q) acc[q] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int q = 0; q < G; ++q) {
+                    acc[q] = mma4x4<T>(make_uint2(wa[u].x, wa[u].y), make_uint2(xr[q][u].x, xr[q][u].y), acc[q]);
+                    acc[q] = mma4x4<T>(make_uint2(wa[u].z, wa[u].w), make_uint2(xr[q][u].z, xr[q][u].w), acc[q]);
+                }
+            // the next quad's loads reuse wa: kept after the MFMAs (one buffer per wave; the
+            // workgroup's NW waves keep the loads in flight)
+            __builtin_amdgcn_sched_barrier(0);
+            const int nrq = t + 1 < QG ? q0 + t + 1 : (grp + gridDim.x) * QG;
+            if (nrq < nquads) load_w(nrq, wa);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < G; ++q) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[q][r] = sum_blocks(acc[q][r]);
+                if (lane < 4) *(f32x4 *)&red[w * QG * 32 + t * 32 + q * 16 + i * 4] = acc[q];
+            }
+        }
+        __syncthreads();
+        for (int o = tid; o < QG * 32; o += 64 * NW) {
+            float v = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < NW; ++ww) v += red[ww * QG * 32 + o];
+            const int t = o >> 5, q = (o >> 4) & 1, c = (o >> 2) & 3, r = o & 3;
+            const int row = 4 * (q0 + t) + r, n = 4 * q + c;
+            if (row < g.M && n < g.N) {
+                T *cp = (T *)g.c + bz * g.c_bs + (int64_t)row * g.c_rs + n * g.c_cs;
+                store_out<T>(g, cp, v, bz * g.bias_bs + (int64_t)row * g.bias_rs + n * g.bias_cs);
+            }
+        }
+        __syncthreads();   // red is rewritten by the next group
+    }
+}
+
+template <class T, bool XKC>
+hipError_t launch_dotx_t(int nw, const GemmArgs &g, dim3 grid, hipStream_t st) {
+    switch (nw) {
+    case 1: hipLaunchKernelGGL((k_dotx<T, 1, XKC>), grid, dim3(64), 0, st, g); break;
+    case 2: hipLaunchKernelGGL((k_dotx<T, 2, XKC>), grid, dim3(128), 0, st, g); break;
+    case 4: hipLaunchKernelGGL((k_dotx<T, 4, XKC>), grid, dim3(256), 0, st, g); break;
+    case 8: hipLaunchKernelGGL((k_dotx<T, 8, XKC>), grid, dim3(512), 0, st, g); break;
+    case 16: hipLaunchKernelGGL((k_dotx<T, 16, XKC>), grid, dim3(1024), 0, st, g); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
+
+int dotx_waves(int64_t K) {
+    const int64_t need = (K + kDotxKW - 1) / kDotxKW;
+    int nw = 1;
+    while (nw < need) nw *= 2;
+    return nw;
+}
+
+bool dotx_offsets_fit(const GemmArgs &g, bool xkc) {
+    const int64_t lim = (int64_t)1 << 31;
+    const int64_t xb = xkc ? (int64_t)8 * g.b_cs + g.K : ((int64_t)g.K + 1) * g.b_rs;
+    return ((int64_t)g.M * g.a_rs + g.K) * 2 < lim && xb * 2 < lim;
+}
 
 // k_thin_dot addresses 16 rows of A (16 vectors of B) plus a K slice from one buffer
 // resource: 31-bit offsets
@@ -338,6 +520,19 @@ bool thin_dot4_offsets_fit(const GemmArgs &g) {
 
 hipError_t launch_thin(int dt, bool ktail, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid,
                        hipStream_t st) {
+    if (t.bm == 4 && t.bn == 8) {   // k_dotx: grid (row-quad groups, 1, batch)
+        // natural vectors: 8 per 16-byte-aligned row; K-contiguous: 16-byte-aligned vector rows
+        const bool ok_b = b_kc ? (g.b_cs & 7) == 0 && ((uintptr_t)g.b & 15) == 0
+                               : g.N == 8 && g.b_cs == 1 && (g.b_rs & 7) == 0 && ((uintptr_t)g.b & 15) == 0;
+        if (!a_kc || !ok_b || g.N > 8 || (g.K & 7) || g.K > (int64_t)kDotxMaxWaves * kDotxKW || g.splits != 1 ||
+            g.persist < 1 || g.batch > 65535 || !dotx_offsets_fit(g, b_kc))
+            return hipErrorInvalidValue;
+        const dim3 grid2(g.persist, 1, g.batch);
+        const int nw = dotx_waves(g.K);
+        if (dt == BF16) return b_kc ? launch_dotx_t<bf16_t, true>(nw, g, grid2, st) : launch_dotx_t<bf16_t, false>(nw, g, grid2, st);
+        if (dt == F16) return b_kc ? launch_dotx_t<f16_t, true>(nw, g, grid2, st) : launch_dotx_t<f16_t, false>(nw, g, grid2, st);
+        return hipErrorInvalidValue;
+    }
     if (t.bm == 4 && t.bn == 16) {   // k_thin_dot4: grid (row-quad workgroups, K slices, batch)
         if (!a_kc || !b_kc || g.N > 16 || (g.K & 7) || g.k_chunk != 512 * kDot4U || g.persist < 1 ||
             !thin_dot4_offsets_fit(g))

@@ -119,6 +119,13 @@ bool thin_dot_offsets_fit(const GemmArgs &g);
 // whether k_thin_dot4 can address the whole matrix and 16 vectors with 31-bit buffer offsets
 bool thin_dot4_offsets_fit(const GemmArgs &g);
 constexpr int kThinDot4Chunk = 4096;   // K per slice of k_thin_dot4 (4 waves x 8 loads x 128 k)
+// k_dotx (up to 8 vectors, the whole K in one workgroup): 16-byte loads per lane per row quad,
+// K per wave, row quads per workgroup group, waves per workgroup at most
+constexpr int kDotxU = 8, kDotxKW = 128 * kDotxU, kDotxQG = 16, kDotxMaxWaves = 16;
+// waves of the k_dotx workgroup for a K (a power of two covering K / 1024)
+int dotx_waves(int64_t K);
+// whether k_dotx addresses the matrix and the vector block with 31-bit buffer offsets
+bool dotx_offsets_fit(const GemmArgs &g, bool xkc);
 }  // namespace m16
 
 // gemv.hip

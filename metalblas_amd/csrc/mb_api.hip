@@ -323,12 +323,14 @@ bool plan_gemv(const Prob &p, Plan &pl) {
 // an explicit wave grid (WM, WN) and schedule are honoured when compiled; BK is fixed by the
 // dtype.  The reference's (BM, BN, NSG) form for backend="mpp_tensor" leaves WM/WN at 0 and
 // gets the default 2 x 2 wave grid.
-// the thin-product tiles (k_thin_dot 64 x 16, k_thin16 32 x 256)
+// the thin-product tiles (k_thin_dot 64 x 16, k_thin_dot4 4 x 16, k_dotx 4 x 8, k_thin16 32 x 256)
 bool thin_tile(const MfmaTile &t) {
-    return (t.bm == 64 && t.bn == 16) || (t.bm == 4 && t.bn == 16) || (t.bm == 32 && t.bn == 256);
+    return (t.bm == 64 && t.bn == 16) || (t.bm == 4 && t.bn == 16) || (t.bm == 4 && t.bn == 8) ||
+           (t.bm == 32 && t.bn == 256);
 }
 
-MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc) {
+// thin_ok: the thin-product tiles are candidates (only for plan_thin_mfma's own request)
+MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc, bool thin_ok) {
     MfmaTile want = {t[0], t[1], 2, 2};
     if (t[3] > 0 && t[4] > 0) {
         want.wm = t[3];
@@ -340,10 +342,11 @@ MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc) {
     int best = 0;
     double bestd = 1e30;
     for (int i = 0; i < n && i < 32; ++i) {
-        // thin tiles: bf16 / fp16, 64 x 16 with both operands K-contiguous, 32 x 256 with A
-        // K-contiguous and B N-contiguous
-        if (thin_tile(list[i]) && ((dt != MB_DTYPE_BF16 && dt != MB_DTYPE_F16) ||
-                                   (list[i].bn == 16 ? !(a_kc && b_kc) : !(a_kc && !b_kc))))
+        // thin tiles: bf16 / fp16, 64 x 16 and 4 x 16 with both operands K-contiguous, 4 x 8
+        // with A K-contiguous, 32 x 256 with A K-contiguous and B N-contiguous
+        if (thin_tile(list[i]) &&
+            (!thin_ok || (dt != MB_DTYPE_BF16 && dt != MB_DTYPE_F16) ||
+             (list[i].bn == 16 ? !(a_kc && b_kc) : list[i].bn == 8 ? !a_kc : !(a_kc && !b_kc))))
             continue;
         double d = fabs(log2((double)list[i].bm / (want.bm > 0 ? want.bm : 1))) +
                    fabs(log2((double)list[i].bn / (want.bn > 0 ? want.bn : 1)));
@@ -459,7 +462,7 @@ int64_t auto_splits(const Prob &p, int64_t tiles, int bk) {
     return s < 1 ? 1 : s;
 }
 
-void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
+void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc, bool thin_ok = false) {
     const int cus = dev_info().cus;
     MfmaTile t;
     bool thin = false;   // the thin-problem tiles below (split for two workgroups per CU)
@@ -468,7 +471,7 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc) {
     // the autotuner puts the tile it measured fastest)
     const bool forced = p.tile[0] > 0 && p.tile[1] > 0;
     if (forced) {
-        t = snap_tile(p.dt, p.tile, a_kc, b_kc);
+        t = snap_tile(p.dt, p.tile, a_kc, b_kc, thin_ok);
     } else if (p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8) {
         // Cost model over the LDS-direct 16-bit tiles, in units of one CU's matrix-core time
         // at the ping-pong kernel's rate (~4.8 TFLOP/s per CU, bf16): rounds x tiles resident
@@ -743,8 +746,9 @@ bool plan_complex(const Prob &p, Plan &pl) {
 
 // Products with a few vectors (2..16) and a large matrix run on the matrix cores, which read
 // the matrix once at HBM speed whatever the vector count (the VALU GEMV kernels spend nv FMAs
-// per matrix element, which outgrows the HBM stream from about 4 vectors up).  Two thin tiles:
-//   64 x 16  (k_thin_dot): matrix = A, K-contiguous; vectors = columns of B;
+// per matrix element, which outgrows the HBM stream from about 4 vectors up).  Thin tiles:
+//   4 x 8    (k_dotx):     matrix = A, K-contiguous; up to 8 vectors = columns of B, whole K;
+//   4 x 16   (k_thin_dot4) and 64 x 16 (k_thin_dot): matrix = A, K-contiguous, K slices;
 //   32 x 256 (k_thin16):   matrix = B, N-contiguous; vectors = rows of A.
 // The other two layouts are the transposed problem of these.  The vectors must be
 // K-contiguous and are copied (nv x K elements) when they are not; a matrix the loaders cannot
@@ -757,8 +761,9 @@ constexpr int kThinMfmaMinNvRows = 2, kThinMfmaMinNvDot = 5;
 
 bool plan_thin_mfma(const Prob &p, Plan &pl) {
     if (p.dt != MB_DTYPE_BF16 && p.dt != MB_DTYPE_F16) return false;
+    MfmaTile req = {0, 0, 0, 0, 0};
     if (p.tile[0] > 0 && p.tile[1] > 0) {   // an explicit tile: only a thin one keeps this plan
-        const MfmaTile req = {p.tile[0], p.tile[1], 0, 0, 0};
+        req = {p.tile[0], p.tile[1], 0, 0, 0};
         if (!thin_tile(req)) return false;
     }
     const bool vec_b = p.N <= p.M;   // vectors are the columns of B
@@ -772,35 +777,54 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     Prob q = p;
     if ((mo == 1) != vec_b) transpose(q);   // K-contiguous matrix as A, N-contiguous as B
     const bool dot = mo == 1;
+    const int64_t cus = dev_info().cus;
+    // k_dotx: up to 8 vectors and K <= 16384 over the whole K in one workgroup (no K slices,
+    // no reduction), when its 16-quad groups alone give every CU a workgroup (or on request);
+    // the vectors stream in place K-contiguous or as the natural 8-wide rows, else they are
+    // copied K-contiguous.  Measured on MI355X (bf16, 16384^2 x 8, per call): 85 us with the
+    // natural vectors against 99.9 us for k_thin_dot4 (vector copy, 4 K slices, reduction).
+    const int64_t groups = ((q.M + 3) / 4 + m16::kDotxQG - 1) / m16::kDotxQG;
+    const bool want_dotx = req.bm == 4 && req.bn == 8, want_other = req.bm > 0 && !want_dotx;
+    bool dotx = dot && nv <= 8 && q.K % 8 == 0 && q.K <= (int64_t)m16::kDotxMaxWaves * m16::kDotxKW &&
+                q.batch <= 65535 && !want_other && (want_dotx || groups * q.batch >= cus);
+    const bool natural = dotx && b_orient(q) == 0 && q.N == 8 && operand_ok(q.b, 0, false, q);
     Plan trial;
-    const int64_t pack_bytes = plan_packs(q, trial, dot ? 2 : 1);   // vectors K-contiguous
+    // vectors K-contiguous (copied when they are not), except the natural rows of k_dotx
+    const int64_t pack_bytes = plan_packs(q, trial, natural ? 0 : (dot ? 2 : 1));
     if (trial.pack[dot ? 0 : 1].on) return false;                    // never copy the matrix
     bool a_kc = false, b_kc = false;
-    if (!mfma_layout_ok(q, a_kc, b_kc) || !(dot ? a_kc && b_kc : a_kc && !b_kc)) return false;
-    // the K-contiguous matrix: k_thin_dot4 (4-row streams) when its 31-bit offsets cover the
-    // matrix, else k_thin_dot
+    if (!mfma_layout_ok(q, a_kc, b_kc) || !(dotx ? a_kc : dot ? a_kc && b_kc : a_kc && !b_kc)) return false;
+    // the K-contiguous matrix otherwise: k_thin_dot4 (4-row streams) when its 31-bit offsets
+    // cover the matrix, else k_thin_dot
     bool dot4 = false;
     if (dot) {
         GemmArgs probe;
         fill_gemm_args(q, probe);
-        dot4 = m16::thin_dot4_offsets_fit(probe);
+        if (dotx) dotx = m16::dotx_offsets_fit(probe, b_kc);
+        if (!dotx) dot4 = m16::thin_dot4_offsets_fit(probe);
     }
-    const MfmaTile t = dot ? (dot4 ? MfmaTile{4, 16, 1, 1, 0} : MfmaTile{64, 16, 4, 1, 0}) : MfmaTile{32, 256, 1, 4, 0};
+    if (natural && !dotx) return false;   // (31-bit offsets only: a matrix of > 1 GiB)
+    const MfmaTile t = dotx  ? MfmaTile{4, 8, m16::kDotxMaxWaves, 1, 0}
+                       : dot ? (dot4 ? MfmaTile{4, 16, 1, 1, 0} : MfmaTile{64, 16, 4, 1, 0})
+                             : MfmaTile{32, 256, 1, 4, 0};
     q.tile[0] = t.bm; q.tile[1] = t.bn; q.tile[2] = 0; q.tile[3] = t.wm; q.tile[4] = t.wn; q.tile[5] = t.sched + 1;
     const int64_t req_split = q.split_req;
     q.split_req = 1;
     pl.pack[0] = trial.pack[0];
     pl.pack[1] = trial.pack[1];
     pl.p = q;
-    plan_mfma(q, pl, a_kc, b_kc);
+    plan_mfma(q, pl, a_kc, b_kc, true);
     if (pl.tile.bm != t.bm || pl.tile.bn != t.bn) return false;
-    if (dot && !m16::thin_dot_offsets_fit(pl.gg)) return false;
+    if (dot && !dotx && !m16::thin_dot_offsets_fit(pl.gg)) return false;
     // K slices: whole macro steps (512) for k_thin_dot, whole stages for k_thin16, at least
     // two / four of them per slice
-    const int64_t cus = dev_info().cus;
     GemmArgs &g = pl.gg;
     int64_t splits;
-    if (dot4) {
+    if (dotx) {
+        splits = 1;
+        g.k_chunk = (int)q.K;
+        g.persist = (int)groups;
+    } else if (dot4) {
         // fixed K slices of m16::kThinDot4Chunk; a persistent grid that walks the row quads, so
         // each workgroup loads its vector slice once: two workgroups per CU, one for matrices
         // of 256 MiB and more.  Measured on MI355X (bf16, 8 vectors, us, two -> one per CU):
@@ -1321,7 +1345,8 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
         info->split_k = pl.gg.splits;
         info->swizzle_log = pl.gg.swz;
         const bool dot4 = pl.tile.bm == 4 && pl.tile.bn == 16;   // k_thin_dot4: 256 threads, persistent
-        info->block = dot4 ? 256 : 64 * pl.tile.wm * pl.tile.wn;
+        const bool dotx = pl.tile.bm == 4 && pl.tile.bn == 8;    // k_dotx: one wave per 1024 of K
+        info->block = dot4 ? 256 : dotx ? 64 * m16::dotx_waves(pl.p.K) : 64 * pl.tile.wm * pl.tile.wn;
         info->grid[0] = pl.gg.persist > 0 ? pl.gg.persist
                                           : (int)(((pl.p.M + pl.tile.bm - 1) / pl.tile.bm) * ((pl.p.N + pl.tile.bn - 1) / pl.tile.bn));
         info->grid[1] = pl.gg.splits;

@@ -691,3 +691,46 @@ def test_deep_k(dev, dtype, shape, layout):
         bias = rand((N,), dtype, g).to(dev)
         got = mb.addmm(bias, ad, bd, beta=0.5, alpha=-2.0)
         assert_parity_full(got, ad, bd, bias=bias, beta=0.5, alpha=-2.0, rows=8, tag=f"deep-K addmm {dtype} {shape}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", ["natural", "kcontig", "six", "xw", "bmm", "addmm"])
+def test_dotx(dev, dtype, case):
+    """k_dotx (4 x 8 tile: up to 8 vectors against a K-contiguous matrix, the whole K in one
+    workgroup): natural 8-wide vector rows and K-contiguous vectors read in place, 6 vectors
+    copied K-contiguous, the transposed form X @ W^T, a batch, the fused epilogue; a partial
+    row quad and group, and K ending inside a wave's piece, inside a 128-k chunk row and at a
+    wave boundary."""
+    g = gen({"natural": 1, "kcontig": 2, "six": 3, "xw": 4, "bmm": 5, "addmm": 6}[case])
+    force = {"tile": (4, 8, 64)}
+    if case == "natural":
+        a, b = rand((2051, 5000), dtype, g), rand((5000, 8), dtype, g)
+    elif case == "kcontig":
+        a, b = rand((2048, 2056), dtype, g), rand((8, 2056), dtype, g).t()
+    elif case == "six":
+        a, b = rand((3000, 16384), dtype, g), rand((16384, 6), dtype, g)
+    elif case == "xw":
+        a, b = rand((8, 4096), dtype, g), rand((2100, 4096), dtype, g).t()
+    elif case == "bmm":
+        a, b = rand((8, 2048, 3072), dtype, g), rand((8, 3072, 8), dtype, g)
+        force = {}
+    else:   # 4096 row quads: 256 groups, picked without a tile request
+        a, b = rand((16384, 4096), dtype, g), rand((4096, 8), dtype, g)
+        force = {}
+    ad, bd = _to(a, dev), _to(b, dev)
+    p = mb.kernels.plan(ad, bd, **force)
+    assert p["family"] == "mfma" and p["tile"][:2] == (4, 8) and p["split_k"] == 1, p
+    assert p["workspace_bytes"] == (16384 * 6 * 2 if case == "six" else 0), p
+    tag = f"dotx {dtype} {case}"
+    if case == "bmm":
+        got = mb.bmm(ad, bd)
+    elif case == "addmm":
+        bias = rand((8,), dtype, g).to(dev)
+        got = mb.addmm(bias, ad, bd, beta=0.5, alpha=-2.0)
+        assert_parity_full(got, ad, bd, bias=bias, beta=0.5, alpha=-2.0, rows=16, tag=tag)
+        return
+    else:
+        got = mb.matmul(ad, bd, **force)
+    assert_parity_full(got, ad, bd, rows=16, tag=tag)
+    again = mb.bmm(ad, bd) if case == "bmm" else mb.matmul(ad, bd, **force)
+    assert torch.equal(got, again), f"{tag}: repeated call differs"

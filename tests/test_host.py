@@ -173,10 +173,26 @@ def test_plan_config2_gemv_families():
     p = _plan(torch.bfloat16, X8, W)
     assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (32, 256)
     assert p.split_k * (n // 256) == 256
-    Xn = torch.empty(n, 8, dtype=torch.bfloat16)   # N-contiguous vectors: copied K-contiguous
+    # W @ X8: k_dotx over the whole K (16 waves x 1024), one 16-quad group per CU, the natural
+    # 8-wide vector rows read in place: no copy, no K slices, no workspace
+    Xn = torch.empty(n, 8, dtype=torch.bfloat16)
     p = _plan(torch.bfloat16, W, Xn)
-    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (4, 16) and p.split_k == 4
-    assert p.workspace_bytes == n * 8 * 2 + 4 * n * 8 * 4   # the vector copy, then the K-slice planes
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (4, 8) and p.split_k == 1
+    assert p.workspace_bytes == 0 and p.block == 1024 and tuple(p.grid) == (256, 1, 1)
+    # K-contiguous vectors stream in place too; 6 natural vectors are copied K-contiguous
+    p = _plan(torch.bfloat16, W, torch.empty(8, n, dtype=torch.bfloat16).t())
+    assert tuple(p.tile[:2]) == (4, 8) and p.workspace_bytes == 0
+    p = _plan(torch.bfloat16, W, torch.empty(n, 6, dtype=torch.bfloat16))
+    assert tuple(p.tile[:2]) == (4, 8) and p.workspace_bytes == n * 6 * 2
+    # 8192 rows give 128 groups (half the CUs): k_thin_dot4 over K slices, the vector copy and
+    # the K-slice planes in the workspace
+    p = _plan(torch.bfloat16, torch.empty(8192, n, dtype=torch.bfloat16), Xn)
+    assert tuple(p.tile[:2]) == (4, 16) and p.split_k == 4
+    assert p.workspace_bytes == n * 8 * 2 + 4 * 8192 * 8 * 4
+    # more than 8 vectors, or K past 16 x 1024: k_thin_dot4
+    assert tuple(_plan(torch.bfloat16, W, torch.empty(n, 12, dtype=torch.bfloat16)).tile[:2]) == (4, 16)
+    assert tuple(_plan(torch.bfloat16, torch.empty(n, 2 * n, dtype=torch.bfloat16),
+                       torch.empty(2 * n, 8, dtype=torch.bfloat16)).tile[:2]) == (4, 16)
     # few vectors against a K-contiguous matrix stay on the VALU GEMV kernel
     assert _lib.FAMILY_NAMES[_plan(torch.bfloat16, W, torch.empty(n, 4, dtype=torch.bfloat16)).family] == "gemv_dot"
     # fp32 stays on the VALU kernels

@@ -75,8 +75,10 @@ def _complex(dev, g, big):
 
 
 def _thin(dev, g, big):
-    n = 16384 if big else 4096
-    W = rand((n, n), torch.bfloat16, g).to(dev)
+    # matrices of 8192 / 4096 rows: k_thin_dot4 over K slices (the vector copy and the K-slice
+    # planes in scratch); at 16384 rows the whole-K kernel needs no scratch
+    m, n = (8192, 16384) if big else (4096, 4096)
+    W = rand((m, n), torch.bfloat16, g).to(dev)
     X = rand((n, 8), torch.bfloat16, g).to(dev)
     return W, X, {}
 
