@@ -335,7 +335,8 @@ __global__ __launch_bounds__(256) void k_thin_dot4(GemmArgs g) {
 // Vectors: K-contiguous (XKC, vector n at n * b_cs + k), or the natural K x 8 row-major block
 // (element (k, n) at k * b_rs + n, 16-byte rows), which each wave transposes through its own
 // LDS region in 256-row phases.  Measured on MI355X, 16384^2 bf16 matrix x 8 vectors:
-// 85 us natural / 82 us K-contiguous (0.79 / 0.82 of 8 TB/s); 92 us with cached loads.
+// 82.2-83.3 us natural / 81.9 us K-contiguous (0.81 / 0.82 of 8 TB/s); 92 us with cached
+// loads, 84-85 us with workgroup barriers between the transpose phases.
 // The host guarantees N <= 8, K % 8 == 0, K <= NW * 1024, batch <= 65535 and 31-bit offsets.
 constexpr int kDotxPH = 256;                   // natural vector rows per LDS transpose phase
 constexpr int kDotxPitch = 2 * kDotxPH + 64;   // bytes per vector row of a phase (conflict-free reads)
@@ -343,6 +344,13 @@ constexpr int kDotxPitch = 2 * kDotxPH + 64;   // bytes per vector row of a phas
 __device__ __forceinline__ uint4 ld_buf_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, int soff) {
     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2);   // nt
     return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// Orders one wave's LDS accesses across its lanes: the LDS executes a wave's instructions in
+// issue order, so only the compiler has to keep them in program order (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_order() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 // sum over the 16 lanes l' with l' % 4 == l % 4 (the k-chunk blocks of a 4 x 4 MFMA result)
 __device__ __forceinline__ float sum_blocks(float v) {
@@ -356,8 +364,10 @@ __device__ __forceinline__ float sum_blocks(float v) {
 template <class T, int NW, bool XKC>
 __global__ __launch_bounds__(64 * NW) void k_dotx(GemmArgs g) {
     constexpr int U = kDotxU, G = 2, KW = kDotxKW, QG = kDotxQG;
-    constexpr int XB = XKC ? 16 : NW * 8 * kDotxPitch, RB = NW * QG * 32 * 4;
-    __shared__ __attribute__((aligned(16))) char lds[XB > RB ? XB : RB];
+    // the natural vectors' transpose regions (one per wave) and the cross-wave sums apart, so
+    // no wave waits for another before its first quad
+    constexpr int XB = XKC ? 0 : NW * 8 * kDotxPitch, RB = NW * QG * 32 * 4;
+    __shared__ __attribute__((aligned(16))) char lds[XB + RB];
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 3, b = lane >> 2;   // row / column index in the 4 x 4 block; block = k chunk
@@ -426,16 +436,16 @@ __global__ __launch_bounds__(64 * NW) void k_dotx(GemmArgs g) {
                 }
             }
             if (ph + 2 < NPH) xload(ph + 2, r0[s], r1[s]);
-            __syncthreads();   // the region is the wave's own; the barrier orders its lanes' LDS writes and reads
+            wave_lds_order();   // the region is the wave's own: its lanes' writes before the reads
 #pragma unroll
             for (int up = 0; up < 2; ++up)
 #pragma unroll
                 for (int q = 0; q < G; ++q)
                     xr[q][2 * ph + up] = *(const uint4 *)(my + (4 * q + i) * kDotxPitch + 256 * up + 16 * b);
-            __syncthreads();   // the next phase overwrites the region
+            wave_lds_order();   // the reads before the next phase's writes
         }
     }
-    float *red = (float *)lds;   // [wave][quad of the group][group q][column i][row r]
+    float *red = (float *)(lds + XB);   // [wave][quad of the group][group q][column i][row r]
     for (; grp * QG < nquads; grp += gridDim.x) {
         const int q0 = grp * QG;
         for (int t = 0; t < QG; ++t) {

@@ -159,7 +159,9 @@ template <> __device__ __forceinline__ void mma16<uint8_t>(i32x16 &c, uint4 a, u
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <class T, int MS> struct AccT { using type = typename AccV<T>::type; };
 template <class T> struct AccT<T, 16> { using type = f32x4; };
-template <class T> __device__ __forceinline__ void mma16x16(f32x4 &c, uint4 a, uint4 b);
+template <> struct AccT<int8_t, 16> { using type = i32x4; };
+template <> struct AccT<uint8_t, 16> { using type = i32x4; };
+template <class T> __device__ __forceinline__ void mma16x16(typename AccT<T, 16>::type &c, uint4 a, uint4 b);
 template <> __device__ __forceinline__ void mma16x16<bf16_t>(f32x4 &c, uint4 a, uint4 b) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
                                                 0);
@@ -167,6 +169,12 @@ template <> __device__ __forceinline__ void mma16x16<bf16_t>(f32x4 &c, uint4 a, 
 template <> __device__ __forceinline__ void mma16x16<f16_t>(f32x4 &c, uint4 a, uint4 b) {
     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+// 8-bit: 16 x 16 x 64, 16 consecutive k per lane (k group l / 16); uint8 runs on the signed form
+// like the 32 x 32 blocks (the products agree modulo 2^8, the width of the uint8 output)
+template <> __device__ __forceinline__ void mma16x16<int8_t>(i32x4 &c, uint4 a, uint4 b) {
+    c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+template <> __device__ __forceinline__ void mma16x16<uint8_t>(i32x4 &c, uint4 a, uint4 b) { mma16x16<int8_t>(c, a, b); }
 template <class T, int MS> __device__ __forceinline__ void mma_blk(typename AccT<T, MS>::type &c, uint4 a, uint4 b) {
     if constexpr (MS == 16)
         mma16x16<T>(c, a, b);
@@ -194,6 +202,13 @@ template <int CPR> __device__ __forceinline__ int swz_mn16(int k) {
     static_assert(CPR >= 16, "rows of at least 256 bytes");
     return 4 * (k & 3) + 2 * ((k >> 3) & 1);
 }
+// 8-bit rows read as 16 x 16 x 64 fragments: a 32-lane slice of one ds_read_b64_tr_b8 reads
+// k-rows k0 + {0..7} and k0 + 16 + {0..7} of one 16-column chunk, which 2 (k & 7) + (k >> 4) & 1
+// puts on 16 distinct 16-byte bank groups.
+template <int CPR> __device__ __forceinline__ int swz_mn16_b8(int k) {
+    static_assert(CPR >= 16, "rows of at least 256 bytes");
+    return 2 * (k & 7) + ((k >> 4) & 1);
+}
 
 __device__ __forceinline__ MB_LDS char *lds_ptr(const char *p) { return (MB_LDS char *)(MB_LDS void *)p; }
 __device__ __forceinline__ uint32_t lds_addr(const char *p) {
@@ -210,10 +225,12 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
     static constexpr int CPR = RB / 16;            // MN-major chunks per row
     static constexpr int EPC = 16 / ES;            // elements per 16-byte chunk
     static_assert(ROWS % 32 == 0 && (KC || RB >= (ES == 2 ? 128 : 64)), "tile rows");
-    static_assert(MS == 32 || (MS == 16 && ES == 2), "16 x 16 blocks are 16-bit only");
+    static_assert(MS == 32 || MS == 16, "32 x 32 or 16 x 16 blocks");
     __device__ __forceinline__ static int swz(int k) {
-        if constexpr (MS == 16)
+        if constexpr (MS == 16 && ES == 2)
             return swz_mn16<CPR>(k);
+        else if constexpr (MS == 16)
+            return swz_mn16_b8<CPR>(k);
         else
             return swz_mn<CPR, ES>(k);
     }
@@ -257,16 +274,22 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
         }
     }
 
-    // 16 x 16 x 32 fragments: lane l reads index l % 16 of block j (16 rows) and the 8 k at
-    // 32 s + 8 (l / 16).  K-major: one 16-byte chunk; M/N-major: two transposing reads of 4 k
-    // (k-row 8 (l / 16) + (l % 16) / 4 + 4 t of columns 4 (l % 4) .. +3).
+    // 16 x 16 fragments: lane l reads index l % 16 of block j (16 rows) and 16 bytes of k for
+    // k group l / 16: 16-bit (16 x 16 x 32) the 8 k at 32 s + 8 (l / 16), 8-bit (16 x 16 x 64)
+    // the 16 k at 64 s + 16 (l / 16).  K-major: one 16-byte chunk; M/N-major: two transposing
+    // reads, of 4 k (16-bit: k-row 8 (l / 16) + (l % 16) / 4 + 4 t of columns 4 (l % 4) .. +3)
+    // or of 8 k (8-bit: k-row 16 (l / 16) + (l % 16) / 2 + 8 t of columns 8 (l % 2) .. +7).
     __device__ __forceinline__ static int frag_base16(int row0, int lane, int j) {
         if constexpr (KC) {
             return (row0 + (lane & 15)) * 128;   // row0 is a multiple of 32
-        } else {
+        } else if constexpr (ES == 2) {
             const int k = 8 * (lane >> 4) + ((lane & 15) >> 2);
             const int col = row0 + 16 * j + 4 * (lane & 3);
             return k * RB + (((col >> 3) ^ swz(k)) << 4) + ((col & 7) << 1);
+        } else {
+            const int k = 16 * (lane >> 4) + ((lane & 15) >> 1);
+            const int col = row0 + 16 * j + 8 * (lane & 1);
+            return k * RB + (((col >> 4) ^ swz(k)) << 4) + (col & 15);
         }
     }
     __device__ __forceinline__ static uint4 frag16(const char *lds, int base, int lane, int s, int j) {
@@ -278,9 +301,16 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
             uint4 out;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const int koff = (32 * s + 4 * t) * RB;
-                bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
-                const uint2 u = __builtin_bit_cast(uint2, v);
+                uint2 u;
+                if constexpr (ES == 2) {
+                    const int koff = (32 * s + 4 * t) * RB;
+                    bf16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((MB_LDS bf16x4 *)(lds_ptr(lds) + base + koff));
+                    u = __builtin_bit_cast(uint2, v);
+                } else {
+                    const int koff = (64 * s + 8 * t) * RB;
+                    i32x2 v = __builtin_amdgcn_ds_read_tr8_b64_v2i32((MB_LDS i32x2 *)(lds_ptr(lds) + base + koff));
+                    u = __builtin_bit_cast(uint2, v);
+                }
                 if (t == 0) {
                     out.x = u.x;
                     out.y = u.y;
@@ -837,9 +867,9 @@ hipError_t launch_deepk16(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hi
 // at the end of odd phases, before the barrier that publishes the stage.
 //
 // MS selects the MFMA block: 32 (32 x 32 x 16 / 32 x 32 x 32 int8, 4 k-steps per stage) or 16
-// (16 x 16 x 32, 2 k-steps).  The 16 x 16 form spends less power per flop, which is what bounds
-// the large products, and runs without the L2 prefetch line: with the loads spread as here
-// the prefetch only adds requests.
+// (16 x 16 x 32 / 16 x 16 x 64 int8, 2 k-steps).  The 16 x 16 form spends less power per flop,
+// which is what bounds the large products, and runs without the L2 prefetch line: with the
+// loads spread as here the prefetch only adds requests.
 //
 // BN = 128 (16 x 16 x 32 blocks only) halves the tile along N, for products with too few
 // 256 x 256 tiles to fill the CUs: 128 x 32 wave tiles, 48 KiB stages.
@@ -1050,9 +1080,12 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     }
 }
 
+// 16 x 16 blocks for every type: 16 x 16 x 32 for the 16-bit floats, 16 x 16 x 64 for 8-bit
+// integers (MI355X, int8 4096^3, per layout: 67.0-69.8 us against 69.4-73.3 us with
+// 32 x 32 x 32 blocks; bit-identical results)
 template <class T, bool KTAIL, int BN = 256>
 hipError_t launch16pp(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
-    constexpr int MS = sizeof(T) == 2 ? 16 : 32;   // 16 x 16 x 32 blocks for the 16-bit types
+    constexpr int MS = 16;
     dim3 block(512);
     if (a_kc && b_kc)
         hipLaunchKernelGGL((k_gemm16pp<T, true, true, KTAIL, MS, BN>), grid, block, 0, st, g);
