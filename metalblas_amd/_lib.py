@@ -240,20 +240,50 @@ def _current_stream(device) -> int:
     return torch._C._cuda_getCurrentRawStream(_device_index(device))
 
 
+# Split-K workspace kept per (device, stream): the kernels of one stream run in order, so a
+# call's scratch is free again for the next call queued on the same stream.  Workspaces above
+# _WS_KEEP bytes are taken from the caching allocator per call instead.
+_WS: dict = {}
+_WS_KEEP = 64 << 20
+
+
+def workspace(idx: int, stream: int, nbytes: int) -> int:
+    """Device address of at least ``nbytes`` of scratch for work queued on ``stream``; the
+    memory stays owned here (kept) or by a tensor the caller must hold until the launch is
+    queued (returned as the second element)."""
+    key = (idx, stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _WS[key] = ws
+    return ws.data_ptr()
+
+
+# 64-bit word indices of the pointer fields in MbGemmDesc (checked at import below)
+W_A, W_B, W_C, W_BIAS, W_WS, W_WS_BYTES = 5, 9, 13, 17, 35, 36
+DESC_WORDS = ctypes.sizeof(MbGemmDesc) // 8
+assert ctypes.sizeof(MbGemmDesc) % 8 == 0 and (MbGemmDesc.a.offset, MbGemmDesc.b.offset, MbGemmDesc.c.offset,
+        MbGemmDesc.bias.offset, MbGemmDesc.workspace.offset, MbGemmDesc.workspace_bytes.offset) == \
+    tuple(8 * w for w in (W_A, W_B, W_C, W_BIAS, W_WS, W_WS_BYTES))
+
+
 def launch(desc: MbGemmDesc, nbytes: int, device) -> None:
     """Queue the product on torch's current stream of ``device`` (the current device; a
-    torch.device or an index) with ``nbytes`` of workspace from torch's stream-ordered caching
-    allocator."""
+    torch.device or an index) with ``nbytes`` of workspace."""
     idx = _device_index(device)
+    stream = torch._C._cuda_getCurrentRawStream(idx)
     ws = None
     if nbytes > 0:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
-        desc.workspace = ws.data_ptr()
+        if nbytes <= _WS_KEEP:
+            desc.workspace = workspace(idx, stream, nbytes)
+        else:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
+            desc.workspace = ws.data_ptr()
         desc.workspace_bytes = nbytes
-    status = (_LIB or load()).mb_gemm(ctypes.byref(desc), torch._C._cuda_getCurrentRawStream(idx))
+    status = (_LIB or load()).mb_gemm(ctypes.byref(desc), stream)
     if status:
         check(status)
-    # ws returns to torch's caching allocator; reuse is ordered on the same stream
+    # a per-call ws returns to torch's caching allocator; reuse is ordered on the same stream
     del ws
 
 

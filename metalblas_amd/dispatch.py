@@ -18,6 +18,8 @@ reference that change no result:
 """
 from __future__ import annotations
 
+import ctypes
+import threading
 from math import prod
 
 import torch
@@ -91,9 +93,32 @@ def _conj_split(t):
 
 # Descriptors already planned (and tuned) for a call signature: the dtype, sizes, strides,
 # pointer alignment classes, flags and scalars.  A hit skips descriptor construction and the
-# tuner; only the four data pointers change between calls.
+# tuner; only the data pointers (and the workspace) change between calls.  Each thread patches
+# its own copy of a descriptor (the C call runs without the GIL), through a view of its 64-bit
+# words.
 _DESC_CACHE: dict = {}
 _DESC_CACHE_CAP = 4096
+_DESC_GEN = [0]   # bumped when _DESC_CACHE is cleared: the threads' copies are dropped too
+_TLS = threading.local()
+_W = ctypes.c_uint64 * _lib.DESC_WORDS
+
+
+def clear_descriptors() -> None:
+    """Forget every cached call signature (the next call of each plans it again)."""
+    _DESC_CACHE.clear()
+    _DESC_GEN[0] += 1
+
+
+def _thread_desc(key, template):
+    """(descriptor, its word view, byref) of this thread for a cached call signature."""
+    mine = getattr(_TLS, "descs", None)
+    if mine is None or mine[0] != _DESC_GEN[0]:
+        mine = _TLS.descs = (_DESC_GEN[0], {})
+    ent = mine[1].get(key)
+    if ent is None:
+        d = _lib.MbGemmDesc.from_buffer_copy(template)
+        ent = mine[1][key] = (d, _W.from_buffer(d), ctypes.byref(d))
+    return ent
 
 
 def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_a=False,
@@ -116,20 +141,31 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
                 _planner.tune(desc, a, b, out, bias)
         hit = (desc, _lib.workspace_bytes(desc))
         if len(_DESC_CACHE) >= _DESC_CACHE_CAP:
-            _DESC_CACHE.clear()
+            clear_descriptors()
         _DESC_CACHE[key] = hit
     template, ws_bytes = hit
-    desc = _lib.MbGemmDesc.from_buffer_copy(template)
-    desc.a.ptr = pa
-    desc.b.ptr = pb
-    desc.c.ptr = pc
-    if bias is not None:
-        desc.bias.ptr = pbias
-    if idx == torch.cuda.current_device():
-        _lib.launch(desc, ws_bytes, idx)
-    else:
+    desc, w, ref = _thread_desc(key, template)
+    w[_lib.W_A] = pa
+    w[_lib.W_B] = pb
+    w[_lib.W_C] = pc
+    w[_lib.W_BIAS] = pbias
+    if idx != torch._C._cuda_getDevice():
         with torch.cuda.device(idx):
             _lib.launch(desc, ws_bytes, idx)
+        return out
+    stream = torch._C._cuda_getCurrentRawStream(idx)
+    ws = None
+    if ws_bytes > 0:
+        if ws_bytes <= _lib._WS_KEEP:
+            w[_lib.W_WS] = _lib.workspace(idx, stream, ws_bytes)
+        else:
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out.device)
+            w[_lib.W_WS] = ws.data_ptr()
+        w[_lib.W_WS_BYTES] = ws_bytes
+    status = (_lib._LIB or _lib.load()).mb_gemm(ref, stream)
+    if status:
+        _lib.check(status)
+    del ws
     return out
 
 

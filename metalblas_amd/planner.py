@@ -37,7 +37,15 @@ _LOCK = threading.Lock()
 _loaded_from: set = set()     # plan-cache files already merged into _PLANS
 
 
+# os.environ's own bytes dictionary (POSIX): reading it skips the str encode / decode of
+# os.environ.get on every call; assignments through os.environ update it
+_ENV_DATA = getattr(os.environ, "_data", None)
+_ENV_KEY = b"METALBLAS_AUTOTUNE"
+
+
 def enabled() -> bool:
+    if isinstance(_ENV_DATA, dict) and os.name == "posix":
+        return _ENV_DATA.get(_ENV_KEY, b"1") != b"0"
     return os.environ.get("METALBLAS_AUTOTUNE", "1") != "0"
 
 

@@ -46,7 +46,7 @@ def test_tuned_plans_match_oracle_and_persist(dev, tmp_path, monkeypatch):
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
     monkeypatch.setenv("METALBLAS_PLAN_CACHE", str(path))
     planner.clear()
-    dispatch._DESC_CACHE.clear()
+    dispatch.clear_descriptors()
     cases = _cases(dev)
     first = []
     for tag, call, (a, b) in cases:
@@ -63,7 +63,7 @@ def test_tuned_plans_match_oracle_and_persist(dev, tmp_path, monkeypatch):
 
     # a fresh process's view: no plan in memory, the file named by METALBLAS_PLAN_CACHE
     planner.clear()
-    dispatch._DESC_CACHE.clear()
+    dispatch.clear_descriptors()
     timed = []
     monkeypatch.setattr(planner, "_autotune", lambda *a, **k: timed.append(1))
     for (tag, call, _), want in zip(cases, first):
@@ -73,14 +73,14 @@ def test_tuned_plans_match_oracle_and_persist(dev, tmp_path, monkeypatch):
     assert not timed, "a plan in the cache file was tuned again"
     assert planner.cached() == {k: (tuple(v) if v is not None else None) for k, v in on_disk.items()}
     planner.clear()
-    dispatch._DESC_CACHE.clear()
+    dispatch.clear_descriptors()
 
 
 def test_tuner_off_keeps_static_plans(dev, monkeypatch):
     monkeypatch.setenv("METALBLAS_AUTOTUNE", "0")
     monkeypatch.delenv("METALBLAS_PLAN_CACHE", raising=False)
     planner.clear()
-    dispatch._DESC_CACHE.clear()
+    dispatch.clear_descriptors()
     called = []
     monkeypatch.setattr(planner, "_autotune", lambda *a, **k: called.append(1))
     g = gen(22)
@@ -89,7 +89,7 @@ def test_tuner_off_keeps_static_plans(dev, monkeypatch):
     got = mb.matmul(a.to(dev), b.to(dev))
     assert_parity(got, a, b, tag="static plan")
     assert not called and not planner.cached()
-    dispatch._DESC_CACHE.clear()
+    dispatch.clear_descriptors()
 
 
 def test_import_name_is_the_references(dev):
