@@ -43,9 +43,30 @@ PEAK_HBM_GBS = 8000.0
 # HBM bytes per launch from rocprofv3 --pmc (FETCH_SIZE x 2 + WRITE_SIZE x 1; the factors
 # come from a 1 GiB copy, which reads as 512 MiB of FETCH_SIZE and 1 GiB of WRITE_SIZE):
 # profiles/gemm_bf16_8192_pmc_traffic.md and profiles/gemv_bf16_16384_pmc_traffic.md
+# HBM-side bytes per launch of each workload's dominant kernel over its timed calls: rocprofv3
+# FETCH_SIZE x 2 + WRITE_SIZE (KiB x 1024; the factors come from a 1 GiB device copy), from
+# profiles/gemm_bf16_8192_counters.md and profiles/configs_counters.md
 TRAFFIC = {
-    "gemm_bf16_8192": 1.7823e9,
-    "gemv_bf16_16384": 5.3745e8,
+    "bf16_gemm_8192": 1.7780e+09,                   # k_gemm16pp<bf16, ...>
+    "gemv_W@x": 5.3750e+08,                         # k_dot_wg
+    "gemv_x@W": 5.4540e+08,                         # k_axpy_band (+ its fp32 planes)
+    "gemv_X8@W": 5.4120e+08,                        # k_thin16 32 x 256
+    "gemv_W@X8": 5.3930e+08,                        # k_dotx
+    "bf16_2048x4096x2048_rm_rm": 1.0920e+08,        # k_gemm16 128 x 128
+    "bf16_2048x4096x2048_rm_cm": 1.0920e+08,
+    "bf16_2048x4096x2048_cm_rm": 1.0920e+08,
+    "bf16_2048x4096x2048_cm_cm": 1.0920e+08,
+    "bf16_2048x4096x2048_row_sliced": 1.0920e+08,
+    "bf16_2048x4096x2048_col_sliced": 1.0920e+08,
+    "bf16_2048x4096x2048_offset17": 1.0920e+08,
+    "bf16_2048x4096x2048_addmm": 1.0940e+08,
+    "f16_bmm_8x512x512x256": 1.6910e+07,            # k_gemm16 (the tuned tile)
+    "f16_bmm_broadcastB": 8.5230e+06,
+    "f16_splitk_128x128x65536": 3.7850e+07,         # the deep-K k_thin16 64 x 64
+    "c64_gemm_2048_conjA": 3.7550e+08,              # k_gemm_mfma<float> after k_cplx_expand
+    "c64_gemv_8192": 5.3760e+08,                    # k_cdot_wg
+    "i8_gemm_4096": 1.1810e+08,                     # k_gemm16pp<int8, ...>
+    "i32_gemm_256": 3.0060e+06,                     # k_gemm_generic<int32, 16>
 }
 
 
@@ -63,6 +84,9 @@ def parse(argv=None):
     p.add_argument("--no-tune", action="store_true",
                    help="static plans only (METALBLAS_AUTOTUNE=0); the default is the library's "
                         "one-shot autotuner, as in the reference")
+    p.add_argument("--calls", type=int, default=0,
+                   help="timed calls of each secondary configuration (default: at least 200); for "
+                        "profiling runs, where every dispatch is collected")
     p.add_argument("--cpu-threads", type=int, default=0,
                    help="threads for the CPU baseline (default: OMP_NUM_THREADS, else all cores)")
     return p.parse_args(argv)
@@ -77,13 +101,13 @@ CFG_WARM_MS = 20.0
 CFG_MIN_CALLS = 200
 
 
-def time_events(torch, fn, steps, warmup, warm_ms=0.0):
-    """ms per call of fn over `steps` calls (at least CFG_MIN_CALLS when warm_ms > 0), after
-    `warmup` untimed calls and, when warm_ms > 0, more untimed calls until the GPU has run them
-    for warm_ms (the clock ramps up over the first milliseconds of work after the host-side
-    set-up, longer than 5 calls of a 50 us product)."""
+def time_events(torch, fn, steps, warmup, warm_ms=0.0, calls=0):
+    """ms per call of fn over `steps` calls (when warm_ms > 0: `calls` calls if given, else at
+    least CFG_MIN_CALLS), after `warmup` untimed calls and, when warm_ms > 0, more untimed calls
+    until the GPU has run them for warm_ms (the clock ramps up over the first milliseconds of
+    work after the host-side set-up, longer than 5 calls of a 50 us product)."""
     if warm_ms > 0:
-        steps = max(steps, CFG_MIN_CALLS)
+        steps = calls if calls > 0 else max(steps, CFG_MIN_CALLS)
     for _ in range(warmup):
         fn()
     if warm_ms > 0:
@@ -417,7 +441,7 @@ def run_group(torch, mb, name, args, results, want, threads, headline_n):
         if name == "headline":
             ms = time_events(torch, w.call, args.steps, args.warmup)
         else:
-            ms = time_events(torch, w.call, args.steps, args.warmup, CFG_WARM_MS)
+            ms = time_events(torch, w.call, args.steps, args.warmup, CFG_WARM_MS, args.calls)
         entry = price(w, ms)
         if not args.no_cpu and w.cpu is not None:
             entry["cpu_baseline"] = cpu_entry(w, threads)
@@ -490,7 +514,7 @@ def main(argv=None):
         result["roofline"] = {
             "bound": "mfma", "achieved": round(tf, 2), "peak": PEAK["bf16"], "unit": "TFLOP/s",
             "frac": round(tf / PEAK["bf16"], 4),
-            "traffic": TRAFFIC["gemm_bf16_8192"] if n == 8192 else None,
+            "traffic": TRAFFIC["bf16_gemm_8192"] if n == 8192 else None,
             "kernel": f"matrix-core GEMM tile {plan['tile'][0]}x{plan['tile'][1]} "
                       f"schedule {'ping-pong' if plan['tile'][5] == 2 else 'interleaved'}",
             "algorithmic_per_launch": f"2*{n}^3 = {w.flops:.4e} flop",
@@ -507,11 +531,11 @@ def main(argv=None):
                                                 "1 warmup + best of >= 3 runs and >= 1 s"}
     if results:
         cfg = {name: e for name, (w, e) in results.items()}
-        if "gemv_W@x" in cfg:
-            cfg["gemv_W@x"]["roofline"]["traffic"] = TRAFFIC["gemv_bf16_16384"]
+        for name, e in cfg.items():
+            e["roofline"]["traffic"] = TRAFFIC.get(name)
         result["configs"] = cfg
         result["configs_timing"] = (f"each config: {args.warmup} warmup calls, {CFG_WARM_MS:g} ms of untimed "
-                                    f"calls, then {max(args.steps, CFG_MIN_CALLS)} timed calls (HIP events)")
+                                    f"calls, then {args.calls or max(args.steps, CFG_MIN_CALLS)} timed calls (HIP events)")
         if result["value"] is None:
             first = next(iter(cfg.values()))
             result.update({"value": first["value"], "unit": first["unit"], "ms_per_step": first["ms"],

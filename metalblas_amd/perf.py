@@ -224,7 +224,10 @@ def pmc_summary(path, kernel, last=0):
         for row in csv.DictReader(f):
             if kernel not in row["Kernel_Name"]:
                 continue
-            per.setdefault(int(row["Dispatch_Id"]), {})[row["Counter_Name"]] = float(row["Counter_Value"])
+            d = per.setdefault(int(row["Dispatch_Id"]), {})
+            d[row["Counter_Name"]] = float(row["Counter_Value"])
+            if row.get("Start_Timestamp") and row.get("End_Timestamp"):
+                d["duration_ns"] = float(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]))
     ids = sorted(per)
     if last > 0:
         ids = ids[-last:]
@@ -233,6 +236,67 @@ def pmc_summary(path, kernel, last=0):
         for c, v in per[i].items():
             out[c] = out.get(c, 0.0) + v / len(ids)
     out["dispatches"] = len(ids)
+    return out
+
+
+# rocprofv3 FETCH_SIZE / WRITE_SIZE scale factors on MI355X: a 1 GiB device copy reads as
+# 512 MiB of FETCH_SIZE and 1 GiB of WRITE_SIZE (bench.py --only copy)
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+
+
+def _trace_last(path, kernel, last):
+    """Durations (ns) of the last ``last`` dispatches of the kernels whose name contains
+    ``kernel`` in a rocprofv3 kernel-trace CSV, and the full name of the first such kernel."""
+    import csv
+    rows, name = [], None
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            n = row.get("Kernel_Name") or row.get("KernelName") or row.get("Name")
+            if kernel not in n:
+                continue
+            name = name or n
+            t0 = int(row.get("Start_Timestamp") or row.get("BeginNs"))
+            rows.append((t0, int(row.get("End_Timestamp") or row.get("EndNs")) - t0))
+    rows.sort()
+    return [d for _, d in (rows[-last:] if last > 0 else rows)], name
+
+
+def counter_report(trace, pmcs, kernel, last, cus=256, simds=1024, alg_bytes=None, alg_ops=None):
+    """Per-dispatch figures of one kernel over its last ``last`` dispatches: duration (kernel
+    trace), shader clock (SQ_BUSY_CU_CYCLES / CUs over the duration), matrix-core busy
+    (SQ_VALU_MFMA_BUSY_CYCLES / (SIMDs x cycles)), LDS instructions and bank-conflict cycles,
+    and HBM-side traffic (FETCH_SIZE x 2 + WRITE_SIZE, in bytes) against the algorithmic bytes."""
+    durs, name = _trace_last(trace, kernel, last)
+    c, ghz = {}, None
+    for path in pmcs:
+        s = pmc_summary(path, kernel, last)
+        if "SQ_BUSY_CU_CYCLES" in s and s.get("duration_ns"):
+            ghz = s["SQ_BUSY_CU_CYCLES"] / cus / s["duration_ns"]   # cycles and duration of one run
+        for k, v in s.items():
+            if k not in ("dispatches", "duration_ns"):
+                c[k] = v
+    out = {"kernel": name, "dispatches": len(durs)}
+    if durs:
+        out["us"] = sum(durs) / len(durs) / 1e3
+    cyc = c.get("SQ_BUSY_CU_CYCLES", 0.0) / cus
+    if ghz:
+        out["ghz"] = ghz
+    if cyc and "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+        out["mfma_busy"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (simds * cyc)
+    if "SQ_INSTS_LDS" in c:
+        out["lds_insts"] = c["SQ_INSTS_LDS"]
+        out["lds_conflict_per_inst"] = c.get("SQ_LDS_BANK_CONFLICT", 0.0) / max(c["SQ_INSTS_LDS"], 1.0)
+    if "FETCH_SIZE" in c or "WRITE_SIZE" in c:
+        out["fetch_bytes"] = c.get("FETCH_SIZE", 0.0) * 1024 * FETCH_SCALE
+        out["write_bytes"] = c.get("WRITE_SIZE", 0.0) * 1024 * WRITE_SCALE
+        out["traffic"] = out["fetch_bytes"] + out["write_bytes"]
+        if alg_bytes:
+            out["traffic_x_alg"] = out["traffic"] / alg_bytes
+        if durs:
+            out["hbm_tbps"] = out["traffic"] / (out["us"] * 1e-6) / 1e12
+    if alg_ops and durs:
+        out["tops"] = alg_ops / (out["us"] * 1e-6) / 1e12
+    out["counters"] = c
     return out
 
 
@@ -325,7 +389,19 @@ def main(argv=None):
     p.add_argument("--kernel", action="append", help="with --trace-summary / --pmc-summary: kernels whose name contains this")
     p.add_argument("--pmc-summary", metavar="CSV", nargs="+",
                    help="average rocprofv3 --pmc counter_collection CSVs per dispatch (of --kernel) and exit")
+    p.add_argument("--counter-report", metavar="CSV", nargs="+",
+                   help="a kernel-trace CSV then --pmc CSVs: one JSON line per --kernel (duration, clock, "
+                        "matrix-core busy, LDS conflicts, traffic over the last N dispatches) and exit")
+    p.add_argument("--alg-bytes", type=float, default=None, help="with --counter-report: algorithmic bytes")
+    p.add_argument("--alg-ops", type=float, default=None, help="with --counter-report: algorithmic flop / op")
     args = p.parse_args(argv)
+    if args.counter_report:
+        import json
+        trace, pmcs = args.counter_report[0], args.counter_report[1:]
+        for kern in args.kernel or [""]:
+            r = counter_report(trace, pmcs, kern, args.last, alg_bytes=args.alg_bytes, alg_ops=args.alg_ops)
+            print(json.dumps(r))
+        return
     if args.pmc_summary:
         kern = (args.kernel or [""])[0]
         merged = {}

@@ -522,3 +522,28 @@ def test_pmc_summary_averages_the_last_dispatches(tmp_path):
     s = perf.pmc_summary(str(f), "k_gemm", last=2)
     assert s["dispatches"] == 2 and s["SQ_A"] == 25 and s["SQ_B"] == 2.5
     assert perf.pmc_summary(str(f), "k_gemm")["SQ_A"] == 20
+
+
+def test_counter_report_derives_clock_busy_and_traffic(tmp_path):
+    """perf.counter_report: duration from the trace, clock from one counter run's own cycles and
+    timestamps, matrix-core busy, conflicts per LDS instruction and the scaled HBM traffic, over
+    the kernel's last N dispatches."""
+    from metalblas_amd import perf
+    tr = tmp_path / "run_kernel_trace.csv"
+    tr.write_text("Kernel_Name,Start_Timestamp,End_Timestamp\n"
+                  "k_x,0,5000\nk_x,10000,12000\nk_x,20000,22000\nother,0,9\n")
+    sq = tmp_path / "sq.csv"
+    rows = ["Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value,Start_Timestamp,End_Timestamp"]
+    for d in (1, 2, 3):   # 2 us dispatches; 256 CUs x 4000 cycles -> 2 GHz; busy 1024 x 1000 / (1024 x 4000)
+        rows += [f"{d},k_x,SQ_BUSY_CU_CYCLES,{256 * 4000},0,2000", f"{d},k_x,SQ_VALU_MFMA_BUSY_CYCLES,{1024 * 1000},0,2000",
+                 f"{d},k_x,SQ_INSTS_LDS,100,0,2000", f"{d},k_x,SQ_LDS_BANK_CONFLICT,50,0,2000"]
+    sq.write_text("\n".join(rows) + "\n")
+    fe = tmp_path / "fetch.csv"
+    fe.write_text("Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n1,k_x,FETCH_SIZE,1\n2,k_x,FETCH_SIZE,3\n3,k_x,FETCH_SIZE,3\n")
+    wr = tmp_path / "write.csv"
+    wr.write_text("Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n1,k_x,WRITE_SIZE,2\n2,k_x,WRITE_SIZE,2\n3,k_x,WRITE_SIZE,2\n")
+    r = perf.counter_report(str(tr), [str(sq), str(fe), str(wr)], "k_x", 2, alg_bytes=8192)
+    assert r["dispatches"] == 2 and r["us"] == 2.0
+    assert abs(r["ghz"] - 2.0) < 1e-9 and abs(r["mfma_busy"] - 0.25) < 1e-12
+    assert r["lds_conflict_per_inst"] == 0.5
+    assert r["fetch_bytes"] == 3 * 1024 * 2 and r["write_bytes"] == 2 * 1024 and r["traffic_x_alg"] == 1.0
