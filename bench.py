@@ -40,9 +40,6 @@ sys.path.insert(0, ROOT)
 PEAK = {"bf16": 2516.6, "f16": 2516.6, "i8": 5033.2, "f32": 157.3}   # TFLOP/s (TOP/s for int8)
 PEAK_HBM_GBS = 8000.0
 
-# HBM bytes per launch from rocprofv3 --pmc (FETCH_SIZE x 2 + WRITE_SIZE x 1; the factors
-# come from a 1 GiB copy, which reads as 512 MiB of FETCH_SIZE and 1 GiB of WRITE_SIZE):
-# profiles/gemm_bf16_8192_pmc_traffic.md and profiles/gemv_bf16_16384_pmc_traffic.md
 # HBM-side bytes per launch of each workload's dominant kernel over its timed calls: rocprofv3
 # FETCH_SIZE x 2 + WRITE_SIZE (KiB x 1024; the factors come from a 1 GiB device copy), from
 # profiles/gemm_bf16_8192_counters.md and profiles/configs_counters.md
