@@ -43,6 +43,43 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+# The compiled fast path of the Python API (csrc/mb_fast.cpp): a PyTorch C++ extension that
+# calls mb_gemm directly for call signatures the Python layer has planned.  Host code only.
+FAST_SRC = os.path.join(CSRC, "mb_fast.cpp")
+
+
+def _fast_target() -> str:
+    import sysconfig
+    return os.path.join(PKG_DIR, "_fast" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def _fast_flags():
+    import sysconfig
+    import torch
+    from torch.utils import cpp_extension as ce
+    tdir = os.path.dirname(torch.__file__)
+    inc = [os.path.join(tdir, "include"), os.path.join(tdir, "include", "torch", "csrc", "api", "include"),
+           "/opt/rocm/include", sysconfig.get_paths()["include"]]
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    cflags = ["-O2", "-std=c++17", "-fPIC", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+              "-DTORCH_API_INCLUDE_EXTENSION_H", "-DTORCH_EXTENSION_NAME=_fast",
+              f"-D_GLIBCXX_USE_CXX11_ABI={abi}"] + [f"-I{d}" for d in inc]
+    tlib = os.path.join(tdir, "lib")
+    ldflags = [f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-ltorch_python",
+               f"-Wl,-rpath,{tlib}", f"-L{PKG_DIR}", "-lmetalblas_hip", "-Wl,-rpath,$ORIGIN"]
+    del ce
+    return cflags, ldflags
+
+
+def _compile_fast(obj):
+    cflags, _ = _fast_flags()
+    cmd = [os.environ.get("CXX", "g++"), *cflags, "-c", FAST_SRC, "-o", obj]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"g++ failed for mb_fast.cpp:\n{proc.stderr[-6000:]}")
+    return obj
+
+
 def _compile(args):
     hipcc, src, obj = args
     cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
@@ -59,16 +96,27 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
     os.makedirs(OBJ_DIR, exist_ok=True)
     objs = [os.path.join(OBJ_DIR, os.path.basename(s) + ".o") for s in srcs]
+    fast_obj = os.path.join(OBJ_DIR, "mb_fast.cpp.o")
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        fast = ex.submit(_compile_fast, fast_obj)
         list(ex.map(_compile, [(hipcc, s, o) for s, o in zip(srcs, objs)]))
+        fast.result()
     out_tmp = LIB_PATH + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr[-6000:]}")
     os.replace(out_tmp, LIB_PATH)
+    target = _fast_target()
+    _, ldflags = _fast_flags()
+    cmd = [os.environ.get("CXX", "g++"), "-shared", "-o", target + ".tmp", fast_obj, *ldflags]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of the fast path failed:\n{proc.stderr[-6000:]}")
+    os.replace(target + ".tmp", target)
     if verbose:
         print(f"built {LIB_PATH}")
+        print(f"built {target}")
     return LIB_PATH
 
 

@@ -19,6 +19,7 @@ reference that change no result:
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from math import prod
 
@@ -26,6 +27,16 @@ import torch
 
 from . import _lib
 from . import planner as _planner
+
+# The compiled fast path (csrc/mb_fast.cpp): matmul / bmm calls whose signature this module has
+# already planned skip the Python checks and ctypes.  Not loaded when METALBLAS_LIB names
+# another build of the library.
+_FAST = None
+if not os.environ.get("METALBLAS_LIB"):
+    try:
+        from . import _fast as _FAST
+    except ImportError:
+        _FAST = None
 
 INTS = (torch.int8, torch.uint8, torch.int16, torch.int32, torch.int64)
 FLOATS = (torch.float32, torch.float16, torch.bfloat16)
@@ -107,6 +118,8 @@ def clear_descriptors() -> None:
     """Forget every cached call signature (the next call of each plans it again)."""
     _DESC_CACHE.clear()
     _DESC_GEN[0] += 1
+    if _FAST is not None:
+        _FAST.clear()
 
 
 def _thread_desc(key, template):
@@ -144,6 +157,9 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
             clear_descriptors()
         _DESC_CACHE[key] = hit
     template, ws_bytes = hit
+    if (_FAST is not None and bias is None and epilogue is None and not conj_a and not conj_b
+            and backend == _lib.BACKEND_AUTO and tile is None and swizzle_log is None):
+        _FAST.register(a, b, out, bytes(template), ws_bytes)   # later calls take the fast path
     desc, w, ref = _thread_desc(key, template)
     w[_lib.W_A] = pa
     w[_lib.W_B] = pb
@@ -319,6 +335,10 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, backend: str | None = None,
            tile: tuple | None = None, swizzle_log: int | None = None,
            out: torch.Tensor | None = None) -> torch.Tensor:
     """Compute ``a @ b`` on the GPU (metalblas/dispatch.py:174-185)."""
+    if _FAST is not None and out is None and backend is None and tile is None and swizzle_log is None:
+        r = _FAST.matmul(a, b)
+        if r is not None:
+            return r
     if a.ndim != 2 or b.ndim != 2:
         return _matmul_nd(a, b, out)
     if _on_device(a) and (a.dtype in COMPLEX_DTYPES or b.dtype in COMPLEX_DTYPES):
@@ -386,6 +406,10 @@ def _batched(a, b, out, Bb, M, N, K, dtype, bias=None, epilogue=None):
 def bmm(a: torch.Tensor, b: torch.Tensor, *,
         out: torch.Tensor | None = None) -> torch.Tensor:
     """Batched 3-D matrix multiplication (metalblas/dispatch.py:211-225)."""
+    if _FAST is not None and out is None:
+        r = _FAST.bmm(a, b)
+        if r is not None:
+            return r
     Bb, M, N, K, dtype = _bmm_shape(a, b, "bmm")
     if Bb == 0 or M == 0 or N == 0:
         return out if out is not None else a.new_empty(Bb, M, N)
