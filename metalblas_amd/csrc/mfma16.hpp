@@ -183,6 +183,10 @@ template <class T, int MS> __device__ __forceinline__ void mma_blk(typename AccT
 }
 
 __device__ __forceinline__ int swz_k(int row) { return (row & 7) ^ ((row >> 3) & 3); }
+// The same for K-major tiles read as 16 x 16 fragments (16 rows x one 16-byte chunk per k group
+// per ds_read_b128): `row & 7` is conflict-free for that pattern (4 LDS cycles per read on
+// MI355X, against 8 with `swz_k`, whose row-bit-3 term collides there).
+__device__ __forceinline__ int swz_k16(int row) { return row & 7; }
 // Chunk swizzle of M/N-major rows.  16-bit: {0, 4, 10, 14}[k & 3]; 8-bit: 2 (k & 7), which
 // puts the 8 k-rows x 2 chunks that a 32-lane slice of one ds_read_b64_tr_b8 touches on 16
 // distinct 16-byte bank groups (for 256-byte rows).  Limited to the chunks of one row.
@@ -226,6 +230,13 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
     static constexpr int EPC = 16 / ES;            // elements per 16-byte chunk
     static_assert(ROWS % 32 == 0 && (KC || RB >= (ES == 2 ? 128 : 64)), "tile rows");
     static_assert(MS == 32 || MS == 16, "32 x 32 or 16 x 16 blocks");
+    // chunk swizzle of K-major rows
+    __device__ __forceinline__ static int swzk(int row) {
+        if constexpr (MS == 16)
+            return swz_k16(row);
+        else
+            return swz_k(row);
+    }
     __device__ __forceinline__ static int swz(int k) {
         if constexpr (MS == 16 && ES == 2)
             return swz_mn16<CPR>(k);
@@ -242,7 +253,7 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
         const int byte = seg * 1024 + lane * 16;
         if constexpr (KC) {
             const int r = byte >> 7, p = (byte >> 4) & 7;
-            const int c = p ^ swz_k(r);
+            const int c = p ^ swzk(r);
             if (r >= rows_left || c * EPC >= k_left) return kOOB;
             return (uint32_t)(((int64_t)r * ld + c * EPC) * ES);
         } else {
@@ -295,7 +306,7 @@ template <int ROWS, int NW, bool KC, int ES = 2, int MS = 32> struct Tile16 {
     __device__ __forceinline__ static uint4 frag16(const char *lds, int base, int lane, int s, int j) {
         if constexpr (KC) {
             const int row = 16 * (j & 1) + (lane & 15);   // the swizzle is periodic in 32 rows
-            const int chunk = (4 * s + (lane >> 4)) ^ swz_k(row);
+            const int chunk = (4 * s + (lane >> 4)) ^ swzk(row);
             return *(const uint4 *)(lds + base + j * 16 * 128 + (chunk << 4));
         } else {
             uint4 out;
