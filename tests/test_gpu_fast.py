@@ -94,3 +94,30 @@ def test_fast_path_falls_through(dev):
     # errors still come from the Python path
     with pytest.raises(AssertionError):
         mb.matmul(a, torch.empty(95, 32, dtype=torch.bfloat16, device=dev))
+
+
+def test_split_k_workspace_is_per_stream(dev):
+    """Split-K products queued on two streams at once, through the compiled path (bmm) and the
+    Python path (addmm): each stream has its own scratch, so every result equals its serial one."""
+    g = gen(77)
+    f16 = torch.float16
+    a1, b1 = rand((1, 128, 16384), f16, g).to(dev), rand((1, 16384, 128), f16, g).to(dev)
+    a2, b2 = rand((1, 128, 16384), f16, g).to(dev), rand((1, 16384, 128), f16, g).to(dev)
+    x1, y1, bias = a1[0], b1[0], rand((128,), f16, g).to(dev)
+    assert mb.kernels.plan(a1, b1)["split_k"] > 1
+    ref1, ref2 = mb.bmm(a1, b1), mb.bmm(a2, b2)
+    ref3 = mb.addmm(bias, x1, y1, beta=0.5, alpha=2.0)
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    outs = []
+    for _ in range(16):
+        with torch.cuda.stream(s1):
+            outs.append((1, mb.bmm(a1, b1)))
+            outs.append((3, mb.addmm(bias, x1, y1, beta=0.5, alpha=2.0)))
+        with torch.cuda.stream(s2):
+            outs.append((2, mb.bmm(a2, b2)))
+            outs.append((3, mb.addmm(bias, x1, y1, beta=0.5, alpha=2.0)))
+    torch.cuda.synchronize()
+    refs = {1: ref1, 2: ref2, 3: ref3}
+    for which, o in outs:
+        assert torch.equal(o, refs[which]), f"stream result {which} differs from the serial one"
