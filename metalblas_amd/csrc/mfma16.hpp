@@ -520,6 +520,77 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccT<T,
     }
 }
 
+// Output tile staged through LDS: the accumulators are converted and written into a BM x BN
+// tile in LDS (row pitch padded by 16 bytes), then the workgroup stores whole rows with one
+// 16-byte store per lane, consecutive lanes on consecutive chunks.  The direct stores of
+// store_tile16 put 16-32 row fragments of 8-16 bytes in every store instruction, which holds
+// products with a short K (where the output dominates the traffic) to about 2.5 TB/s of writes.
+// Taken for plain row-major outputs: no split-K planes, no epilogue, 16-byte aligned rows.
+template <class T, int BM, int BN> struct CStage {
+    static_assert(sizeof(T) <= 2, "the staged store packs 4 outputs into 8 or 4 bytes");
+    static constexpr int PITCH = BN * (int)sizeof(T) + 16;
+    static constexpr int BYTES = BM * PITCH;
+};
+
+template <class T> __device__ __forceinline__ bool staged_store_ok(const GemmArgs &g) {
+    return g.splits <= 1 && !g.planes && !g.epilogue && g.c_cs == 1 && ((g.c_rs * (int64_t)sizeof(T)) & 15) == 0 &&
+           (g.batch == 1 || ((g.c_bs * (int64_t)sizeof(T)) & 15) == 0) && (((uintptr_t)g.c) & 15) == 0;
+}
+
+// this wave's accumulators (the block layout of store_tile16) into the staged tile; mw / nw are
+// tile-relative
+template <class T, int TM, int TN, int MS, int PITCH>
+__device__ __forceinline__ void stage_acc(char *ct, typename AccT<T, MS>::type (&acc)[TN][TM], int mw, int nw,
+                                          int lane) {
+    constexpr int NQ = MS * MS / 256;
+    const int mrow = lane % MS, nsub = 4 * (lane / MS);
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                const int row = mw + j * MS + mrow, col = nw + i * MS + 8 * q + nsub;
+                T o[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
+                char *dst = ct + row * PITCH + col * (int)sizeof(T);
+                if constexpr (sizeof(T) == 2) {
+                    uint2 u;
+                    __builtin_memcpy(&u, o, 8);
+                    *(uint2 *)dst = u;
+                } else {
+                    uint32_t u;
+                    __builtin_memcpy(&u, o, 4);
+                    *(uint32_t *)dst = u;
+                }
+            }
+}
+
+// the staged tile out to C rows m0.., columns n0.. (16 bytes per thread and step; the ragged
+// right edge element by element)
+template <class T, int BM, int BN, int NT>
+__device__ __forceinline__ void store_staged(const GemmArgs &g, const char *ct, int m0, int n0, int bz, int tid) {
+    constexpr int PITCH = CStage<T, BM, BN>::PITCH;
+    constexpr int EPC = 16 / (int)sizeof(T);
+    constexpr int CPR = BN / EPC;
+    T *Cb = (T *)g.c + bz * g.c_bs;
+    const int rows = min(BM, g.M - m0), cols = min(BN, g.N - n0);
+    for (int c = tid; c < rows * CPR; c += NT) {
+        const int r = c / CPR, col = (c % CPR) * EPC;
+        if (col >= cols) continue;
+        const uint4 v = *(const uint4 *)(ct + r * PITCH + col * (int)sizeof(T));
+        T *dst = Cb + (int64_t)(m0 + r) * g.c_rs + n0 + col;
+        if (col + EPC <= cols) {
+            *(uint4 *)dst = v;
+        } else {
+            T e[EPC];
+            __builtin_memcpy(e, &v, 16);
+            for (int k = 0; k < cols - col; ++k) dst[k] = e[k];
+        }
+    }
+}
+
 // KTAIL: some K slice ends inside a stage (its last stage is zero-filled past the
 // edge).  Without it the main loop carries no edge logic.
 template <class T, int BM, int BN, int WM, int WN, bool A_KC, bool B_KC, bool KTAIL>
@@ -536,8 +607,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     // LDS read instructions per k-step (a transposing fragment takes two)
     constexpr int NREAD_RAW = TM * (A_KC ? 1 : 2) + TN * (B_KC ? 1 : 2);
     constexpr int NREAD = NREAD_RAW < TM * TN ? NREAD_RAW : TM * TN;
+    using CS = CStage<T, BM, BN>;
+    constexpr int SMEM = 2 * STAGE > CS::BYTES ? 2 * STAGE : CS::BYTES;
 
-    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
     __shared__ __attribute__((aligned(256))) char pf_junk[256];
     const uint32_t smem_lds = lds_addr(smem);   // LDS byte address of smem
     const uint32_t junk_lds = lds_addr(pf_junk);
@@ -683,7 +756,14 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
             mma_step(1);
         }
 
-        store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        if (staged_store_ok<T>(g)) {
+            __syncthreads();   // every wave is done with the operand stages
+            stage_acc<T, TM, TN, 32, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
+            __syncthreads();
+            store_staged<T, BM, BN, 64 * NW>(g, smem, m0, n0, bz, tid);
+        } else {
+            store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        }
         __syncthreads();   // LDS reuse by the next batch iteration
     }
 }
@@ -895,8 +975,10 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     using TA = Tile16<BM, NW, A_KC, ES, MS>;
     using TB = Tile16<BN, NW, B_KC, ES, MS>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
+    using CS = CStage<T, BM, BN>;
+    constexpr int SMEM = 2 * STAGE > CS::BYTES ? 2 * STAGE : CS::BYTES;
 
-    __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) char smem[SMEM];
     __shared__ __attribute__((aligned(256))) char pf_junk[256];
     const uint32_t smem_lds = lds_addr(smem);
     const uint32_t junk_lds = lds_addr(pf_junk);
@@ -1086,7 +1168,14 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 }
             }
         }
-        store_tile16<T, TM, TN, MS>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        if (staged_store_ok<T>(g)) {
+            __syncthreads();   // both wave groups are done with the operand stages
+            stage_acc<T, TM, TN, MS, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
+            __syncthreads();
+            store_staged<T, BM, BN, 512>(g, smem, m0, n0, bz, tid);
+        } else {
+            store_tile16<T, TM, TN, MS>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+        }
         __syncthreads();   // LDS reuse by the next batch iteration
     }
 }
