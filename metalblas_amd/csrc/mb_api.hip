@@ -768,12 +768,34 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
     }
     const bool vec_b = p.N <= p.M;   // vectors are the columns of B
     const int64_t nv = vec_b ? p.N : p.M, wide = vec_b ? p.M : p.N;
-    if (nv > 16 || wide < 2048 || p.K < 2048) return false;
     const int mo = vec_b ? a_orient(p) : b_orient(p);   // the matrix: 1 = K-contiguous
     if (mo < 0) return false;
-    // K-contiguous matrix: the VALU kernels stream 2 and 4 vectors faster (95-97 us vs
-    // ~111 us); 3 vectors have no fast VALU form (347 us)
-    if (mo == 1 ? (nv < kThinMfmaMinNvDot && nv != 3) : nv < kThinMfmaMinNvRows) return false;
+    // the dot tiles take up to 16 vectors, the 32 x 256 tile up to 32
+    if (nv > (mo == 1 ? 16 : 32)) return false;
+    if (req.bm == 0) {   // the automatic choice (an explicit thin tile skips these)
+        if (mo == 1) {
+            if (nv > 16 || wide < 2048 || p.K < 2048) return false;
+            // K-contiguous matrix: the VALU kernels stream 2 and 4 vectors faster (95-97 us vs
+            // ~111 us); 3 vectors have no fast VALU form (347 us)
+            if (nv < kThinMfmaMinNvDot && nv != 3) return false;
+        } else {
+            if (nv < kThinMfmaMinNvRows) return false;
+            // N-contiguous matrix on the 32 x 256 tile.  Up to 16 vectors: a large matrix
+            // (>= 32 MiB over >= 8 tiles), also with a short K or a batch, where the VALU
+            // kernel's K slices write fp32 planes of nv x N per slice.  17-32 vectors (where
+            // the alternative is the 64 x 128 tile with half its rows idle): a matrix of
+            // >= 256 MiB, or enough tiles for every CU without K slices.  Measured on MI355X
+            // (bf16, us, VALU or 64 x 128 -> 32 x 256): 16 x 65536 x 1024 71.6 -> 22.5,
+            // bmm 64 x 16 x 4096 x 512 109 -> 60, 512 x 16 x 1024 x 512 316 -> 101,
+            // 32 x 16384^2 104 -> 89, bmm 256 x 32 x 2048 x 512 116 -> 107; kept:
+            // 32 x 8192^2 29.7 (34.0), 32 x 16384 x 4096 27.5 (31.1).
+            const int64_t tiles = (wide + 255) / 256 * p.batch;
+            const int64_t mat_bytes = wide * p.K * p.batch * dtype_size(p.dt);
+            const bool take = nv <= 16 ? (wide >= 2048 && p.K >= 2048) || (mat_bytes >= (32LL << 20) && tiles >= 8)
+                                       : mat_bytes >= (256LL << 20) || tiles >= dev_info().cus;
+            if (!take) return false;
+        }
+    }
     Prob q = p;
     if ((mo == 1) != vec_b) transpose(q);   // K-contiguous matrix as A, N-contiguous as B
     const bool dot = mo == 1;
@@ -883,7 +905,7 @@ int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
         return MB_OK;
     }
     const bool thin = p.M <= 16 || p.N <= 16;
-    if (p.backend == MB_BACKEND_AUTO && thin && allow_ws) {
+    if (p.backend == MB_BACKEND_AUTO && (p.M <= 32 || p.N <= 32) && allow_ws) {
         Plan tp = pl;
         if (plan_thin_mfma(p, tp)) {
             pl = tp;

@@ -425,6 +425,36 @@ def test_thin_matrix_cores_more(dev, case):
         assert_parity(mb.matmul(a.to(dev), b.to(dev)), a, b, tag="thin odd K")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
+@pytest.mark.parametrize("case", [(16, 16, 2048, 512, None), (64, 24, 1024, 256, None), (256, 16, 1024, 64, None),
+                                  (1, 16, 16384, 1024, None), (1, 32, 2304, 520, (32, 256)),
+                                  (1, 16, 1024, 40, (32, 256)), (1, 5, 1000, 136, (32, 256))], ids=str)
+@pytest.mark.parametrize("a_layout", ["r", "c"])
+def test_thin_rows_batched_and_short_k(dev, dtype, case, a_layout):
+    """The 32 x 256 matrix-core tile for up to 32 vectors (rows of A) over an N-contiguous
+    matrix: batched and short-K products (no K slices, a single stage), a ragged K (partial
+    stage), a ragged N edge, and A copied K-contiguous when it is column-major.  Explicit tile
+    requests (2-D) skip the size rules; the automatic cases are ones the planner routes to this
+    tile."""
+    B, M, N, K, tile = case
+    g = gen(M * 7 + K)
+    if a_layout == "r":
+        a = rand((B, M, K), dtype, g)
+    else:
+        a = rand((B, K, M), dtype, g).transpose(1, 2)
+    b = rand((B, K, N), dtype, g)
+    if B == 1:
+        a, b = a[0], b[0]
+    ad, bd = _to(a, dev), _to(b, dev)
+    p = mb.kernels.plan(ad, bd, tile=tile)
+    assert p["family"] == "mfma" and p["tile"][:2] == (32, 256), p
+    if B > 1:
+        got = mb.bmm(ad, bd)
+    else:
+        got = mb.matmul(ad, bd, tile=tile) if tile else mb.matmul(ad, bd)
+    assert_parity(got, a, b, tag=f"thin rows {dtype} {case} A {a_layout}")
+
+
 @pytest.mark.parametrize("n", [8192, 16384])
 def test_gemv_config2_sizes(dev, n):
     """BASELINE config 2 at full size: y = W @ x, x @ W and 8-vector thin products,
