@@ -44,7 +44,7 @@ constexpr TileEntry kTiles16[] = {
     // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 and
     // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 (A K-contiguous, B
     // N-contiguous), k_dotx 4 x 8 (A K-contiguous, up to 16 waves over the whole K)
-    {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},  {4, 16, 1, 1, 0},  {4, 8, 16, 1, 0},
+    {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},  {32, 128, 1, 4, 0}, {4, 16, 1, 1, 0},  {4, 8, 16, 1, 0},
     // the deep-K schedule of the 64 x 64 tile (bf16 / fp16): few output tiles, many K slices
     {64, 64, 2, 2, 2},
 };
@@ -106,7 +106,8 @@ hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const Ge
         const int es = dtype_size(dt), bk = 128 / es;
         if (m16_offsets_fit(t, a_kc, b_kc, g, es)) {
             const bool whole = (g.k_chunk % bk) == 0 && (g.K % bk) == 0;
-            if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && t.bn == 256) || (t.bm == 4 && t.bn == 16) || dotx)
+            if ((t.bm == 64 && t.bn == 16) || (t.bm == 32 && (t.bn == 256 || t.bn == 128)) || (t.bm == 4 && t.bn == 16) ||
+                dotx)
                 return m16::launch_thin(dt, !whole, t, a_kc, b_kc, g, grid, st);
             if (t.sched == 2) {   // deep-K: a 1-D grid of (K slice, tile) workgroups
                 const dim3 g1(tiles * g.splits, 1, grid.z);

@@ -323,10 +323,11 @@ bool plan_gemv(const Prob &p, Plan &pl) {
 // an explicit wave grid (WM, WN) and schedule are honoured when compiled; BK is fixed by the
 // dtype.  The reference's (BM, BN, NSG) form for backend="mpp_tensor" leaves WM/WN at 0 and
 // gets the default 2 x 2 wave grid.
-// the thin-product tiles (k_thin_dot 64 x 16, k_thin_dot4 4 x 16, k_dotx 4 x 8, k_thin16 32 x 256)
+// the thin-product tiles (k_thin_dot 64 x 16, k_thin_dot4 4 x 16, k_dotx 4 x 8, k_thin16 32 x 256
+// and 32 x 128)
 bool thin_tile(const MfmaTile &t) {
     return (t.bm == 64 && t.bn == 16) || (t.bm == 4 && t.bn == 16) || (t.bm == 4 && t.bn == 8) ||
-           (t.bm == 32 && t.bn == 256);
+           (t.bm == 32 && (t.bn == 256 || t.bn == 128));
 }
 
 // thin_ok: the thin-product tiles are candidates (only for plan_thin_mfma's own request)
@@ -826,9 +827,26 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
         if (!dotx) dot4 = m16::thin_dot4_offsets_fit(probe);
     }
     if (natural && !dotx) return false;   // (31-bit offsets only: a matrix of > 1 GiB)
+    // the N-contiguous matrix: 32 x 128 (an 80 KiB ring, two workgroups per CU, so one's
+    // prologue overlaps the other's stream) when the 32 x 256 tile would stream at most 512 of K
+    // per workgroup or split K; else 32 x 256.  Measured on MI355X (bf16, us, 32 x 256 ->
+    // 32 x 128): bmm 64 x 8 x 4096 x 512 58.3 -> 47.9, bmm 32 x 16 x 8192 x 256 38.7 -> 29.9,
+    // 16 x 16384 x 2048 17.2 -> 15.3, 8 x 16384^2 85.7 -> 85.2; kept: bmm 128 x 16 x 2048 x 1024
+    // 88.6 (95.2), 16 x 65536 x 1024 22.5 (23.0).
+    int rows_bn = 256;
+    if (!dot && !dotx) {
+        if (req.bm == 32) {
+            rows_bn = req.bn == 128 ? 128 : 256;
+        } else {
+            const int64_t tiles256 = (q.N + 255) / 256 * q.batch;
+            const int64_t max_splits = q.K / (4 * (128 / dtype_size(q.dt)));
+            const bool split = q.split_req > 1 || (tiles256 < cus && max_splits > 1);
+            if (split || q.K <= 512) rows_bn = 128;
+        }
+    }
     const MfmaTile t = dotx  ? MfmaTile{4, 8, m16::kDotxMaxWaves, 1, 0}
                        : dot ? (dot4 ? MfmaTile{4, 16, 1, 1, 0} : MfmaTile{64, 16, 4, 1, 0})
-                             : MfmaTile{32, 256, 1, 4, 0};
+                             : MfmaTile{32, rows_bn, 1, 4, 0};
     q.tile[0] = t.bm; q.tile[1] = t.bn; q.tile[2] = 0; q.tile[3] = t.wm; q.tile[4] = t.wn; q.tile[5] = t.sched + 1;
     const int64_t req_split = q.split_req;
     q.split_req = 1;
@@ -860,7 +878,7 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
         g.persist = (int)(wgs < quads ? wgs : quads);
     } else {
         const int64_t unit = dot ? 512 : 128 / dtype_size(q.dt);
-        const int64_t tiles = (dot ? (q.M + 63) / 64 : (q.N + 255) / 256) * q.batch;
+        const int64_t tiles = (dot ? (q.M + 63) / 64 : (q.N + t.bn - 1) / t.bn) * q.batch;
         splits = req_split > 0 ? req_split : (cus + tiles - 1) / tiles;
         const int64_t maxs = q.K / ((dot ? 2 : 4) * unit);
         if (req_split <= 0 && splits > maxs) splits = maxs;

@@ -917,8 +917,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_thin16(GemmArgs g) {
 // per CU.
 template <class T, bool KTAIL>
 hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
-    if (!(t.bm == 32 && t.bn == 256 && t.wm == 1 && t.wn == 4 && a_kc && !b_kc)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((k_thin16<T, 32, 256, 1, 4, true, false, KTAIL, 4, false, false, true>), grid, dim3(256), 0, st, g);
+    if (!(t.bm == 32 && (t.bn == 256 || t.bn == 128) && t.wm == 1 && t.wn == 4 && a_kc && !b_kc))
+        return hipErrorInvalidValue;
+    if (t.bn == 256)
+        hipLaunchKernelGGL((k_thin16<T, 32, 256, 1, 4, true, false, KTAIL, 4, false, false, true>), grid, dim3(256), 0, st, g);
+    else
+        hipLaunchKernelGGL((k_thin16<T, 32, 128, 1, 4, true, false, KTAIL, 4, false, false, true>), grid, dim3(256), 0, st, g);
     return hipGetLastError();
 }
 

@@ -397,7 +397,7 @@ def test_thin_matrix_cores(dev, dtype, nv, layout, side):
     p = mb.kernels.plan(ad, bd)
     dot = (side == "N" and layout[0] == "r") or (side == "M" and layout[1] == "c")   # K-contiguous matrix
     if (nv >= 5 or nv == 3) if dot else nv >= 2:
-        assert p["family"] == "mfma" and p["tile"][:2] == ((4, 16) if dot else (32, 256)), p
+        assert p["family"] == "mfma" and (p["tile"][:2] == (4, 16) if dot else p["tile"][0] == 32), p
     got = mb.matmul(ad, bd)
     assert_parity(got, a, b, tag=f"thin mfma {dtype} nv={nv} {layout} {side}")
 
@@ -427,15 +427,17 @@ def test_thin_matrix_cores_more(dev, case):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("case", [(16, 16, 2048, 512, None), (64, 24, 1024, 256, None), (256, 16, 1024, 64, None),
-                                  (1, 16, 16384, 1024, None), (1, 32, 2304, 520, (32, 256)),
-                                  (1, 16, 1024, 40, (32, 256)), (1, 5, 1000, 136, (32, 256))], ids=str)
+                                  (128, 16, 1024, 1024, None), (1, 16, 16384, 1024, None),
+                                  (1, 32, 2304, 520, (32, 256)), (1, 16, 1024, 40, (32, 256)),
+                                  (1, 5, 1000, 136, (32, 256)), (1, 32, 2304, 520, (32, 128)),
+                                  (1, 16, 1024, 40, (32, 128)), (1, 5, 1000, 136, (32, 128))], ids=str)
 @pytest.mark.parametrize("a_layout", ["r", "c"])
 def test_thin_rows_batched_and_short_k(dev, dtype, case, a_layout):
-    """The 32 x 256 matrix-core tile for up to 32 vectors (rows of A) over an N-contiguous
-    matrix: batched and short-K products (no K slices, a single stage), a ragged K (partial
-    stage), a ragged N edge, and A copied K-contiguous when it is column-major.  Explicit tile
-    requests (2-D) skip the size rules; the automatic cases are ones the planner routes to this
-    tile."""
+    """The 32 x 256 and 32 x 128 matrix-core tiles for up to 32 vectors (rows of A) over an
+    N-contiguous matrix: batched and short-K products (no K slices, a single stage), a ragged K
+    (partial stage), a ragged N edge, and A copied K-contiguous when it is column-major.
+    Explicit tile requests (2-D) skip the size rules; the automatic cases are ones the planner
+    routes to these tiles."""
     B, M, N, K, tile = case
     g = gen(M * 7 + K)
     if a_layout == "r":
@@ -447,7 +449,8 @@ def test_thin_rows_batched_and_short_k(dev, dtype, case, a_layout):
         a, b = a[0], b[0]
     ad, bd = _to(a, dev), _to(b, dev)
     p = mb.kernels.plan(ad, bd, tile=tile)
-    assert p["family"] == "mfma" and p["tile"][:2] == (32, 256), p
+    assert p["family"] == "mfma" and p["tile"][0] == 32 and p["tile"][1] == (tile[1] if tile else p["tile"][1]), p
+    assert p["tile"][1] in (128, 256), p
     if B > 1:
         got = mb.bmm(ad, bd)
     else:

@@ -168,11 +168,18 @@ def test_plan_config2_gemv_families():
     assert _lib.FAMILY_NAMES[p.family] == "gemv_axpy" and p.tile[2] == 1
     # x @ W streams W along its rows: split over K to fill 256 CUs, partials in the workspace
     assert p.split_k > 1 and p.workspace_bytes == p.split_k * n * 4
-    # 8 vectors: the thin matrix-core tiles, one workgroup per CU
+    # 8 vectors: the thin matrix-core tile 32 x 128 over K slices, two workgroups per CU
     X8 = torch.empty(8, n, dtype=torch.bfloat16)
     p = _plan(torch.bfloat16, X8, W)
-    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (32, 256)
-    assert p.split_k * (n // 256) == 256
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (32, 128)
+    assert p.split_k * (n // 128) == 256
+    # batched vectors with a short K: 32 x 128, no K slices; K = 1024 unsplit: 32 x 256
+    p = _plan(torch.bfloat16, torch.empty(64, 8, 512, dtype=torch.bfloat16),
+              torch.empty(64, 512, 4096, dtype=torch.bfloat16))
+    assert tuple(p.tile[:2]) == (32, 128) and p.split_k == 1 and p.workspace_bytes == 0
+    p = _plan(torch.bfloat16, torch.empty(128, 16, 1024, dtype=torch.bfloat16),
+              torch.empty(128, 1024, 2048, dtype=torch.bfloat16))
+    assert tuple(p.tile[:2]) == (32, 256) and p.split_k == 1
     # W @ X8: k_dotx over the whole K (16 waves x 1024), one 16-quad group per CU, the natural
     # 8-wide vector rows read in place: no copy, no K slices, no workspace
     Xn = torch.empty(n, 8, dtype=torch.bfloat16)
