@@ -384,6 +384,7 @@ def main(argv=None):
     p.add_argument("--cool", type=float, default=0.0, help="sleep this ratio of each benchmark's time after it")
     p.add_argument("--report", action="store_true", help="write profiles/shape_sweep_<gpu>.md (bf16)")
     p.add_argument("--bmm", action="store_true", help="the bmm shape groups instead of the matmul ones")
+    p.add_argument("--shape", metavar="MxNxK", help="one shape instead of the groups (with --layout: each layout)")
     p.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel trace and exit")
     p.add_argument("--last", type=int, default=0, help="with --trace-summary: each kernel's last N dispatches")
     p.add_argument("--kernel", action="append", help="with --trace-summary / --pmc-summary: kernels whose name contains this")
@@ -434,6 +435,14 @@ def main(argv=None):
         for dt in dtypes:
             for g in groups:
                 run_bmm_group(g, BMM_SHAPES[g], dt, check=args.check)
+        return
+    if args.shape:
+        shape = tuple(int(v) for v in args.shape.lower().split("x"))
+        if len(shape) != 3:
+            p.error("--shape takes MxNxK")
+        for dt in dtypes:
+            for lay in layouts or [None]:
+                run_group("shape", [shape], dt, layout=lay, check=args.check, cool=args.cool)
         return
     groups = list(SHAPES) if args.group == "all" else [args.group]
     for dt in dtypes:
