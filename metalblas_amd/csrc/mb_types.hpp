@@ -209,6 +209,7 @@ struct GemmArgs {
                          // reduction kernel finishes the output)
     int32_t bias_vec;    // bias rows read as 4-element vectors (contiguous, 4-element aligned)
     int32_t persist;     // workgroups of a persistent grid that loops over tiles (0: one per tile)
+    int32_t c_stream;    // output larger than the last-level cache: non-temporal output stores
     EpiScalars s;
 };
 

@@ -567,9 +567,22 @@ __device__ __forceinline__ void stage_acc(char *ct, typename AccT<T, MS>::type (
             }
 }
 
+// element k of a 16-byte chunk, picked from registers (a local array here would be placed in
+// LDS by the compiler, 16 bytes per thread, and cost workgroups per CU)
+template <class T> __device__ __forceinline__ T chunk_elem(const uint4 &v, int k) {
+    constexpr int PER = 4 / (int)sizeof(T);
+    const int w = k / PER;
+    const uint32_t word = w == 0 ? v.x : w == 1 ? v.y : w == 2 ? v.z : v.w;
+    const uint32_t bits = word >> (8 * (int)sizeof(T) * (k % PER));
+    if constexpr (sizeof(T) == 2)
+        return __builtin_bit_cast(T, (uint16_t)bits);
+    else
+        return __builtin_bit_cast(T, (uint8_t)bits);
+}
+
 // the staged tile out to C rows m0.., columns n0.. (16 bytes per thread and step; the ragged
-// right edge element by element)
-template <class T, int BM, int BN, int NT>
+// right edge element by element); STREAM: non-temporal stores (an output larger than the cache)
+template <class T, int BM, int BN, int NT, bool STREAM>
 __device__ __forceinline__ void store_staged(const GemmArgs &g, const char *ct, int m0, int n0, int bz, int tid) {
     constexpr int PITCH = CStage<T, BM, BN>::PITCH;
     constexpr int EPC = 16 / (int)sizeof(T);
@@ -582,11 +595,14 @@ __device__ __forceinline__ void store_staged(const GemmArgs &g, const char *ct, 
         const uint4 v = *(const uint4 *)(ct + r * PITCH + col * (int)sizeof(T));
         T *dst = Cb + (int64_t)(m0 + r) * g.c_rs + n0 + col;
         if (col + EPC <= cols) {
-            *(uint4 *)dst = v;
+            if constexpr (STREAM) {
+                typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+                __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, (u32x4_t *)dst);
+            } else {
+                *(uint4 *)dst = v;
+            }
         } else {
-            T e[EPC];
-            __builtin_memcpy(e, &v, 16);
-            for (int k = 0; k < cols - col; ++k) dst[k] = e[k];
+            for (int k = 0; k < cols - col; ++k) dst[k] = chunk_elem<T>(v, k);
         }
     }
 }
@@ -760,7 +776,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
             __syncthreads();   // every wave is done with the operand stages
             stage_acc<T, TM, TN, 32, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
             __syncthreads();
-            store_staged<T, BM, BN, 64 * NW>(g, smem, m0, n0, bz, tid);
+            if (g.c_stream)
+                store_staged<T, BM, BN, 64 * NW, true>(g, smem, m0, n0, bz, tid);
+            else
+                store_staged<T, BM, BN, 64 * NW, false>(g, smem, m0, n0, bz, tid);
         } else {
             store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         }
@@ -1176,7 +1195,10 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             __syncthreads();   // both wave groups are done with the operand stages
             stage_acc<T, TM, TN, MS, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
             __syncthreads();
-            store_staged<T, BM, BN, 512>(g, smem, m0, n0, bz, tid);
+            if (g.c_stream)
+                store_staged<T, BM, BN, 512, true>(g, smem, m0, n0, bz, tid);
+            else
+                store_staged<T, BM, BN, 512, false>(g, smem, m0, n0, bz, tid);
         } else {
             store_tile16<T, TM, TN, MS>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         }

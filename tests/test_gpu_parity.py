@@ -207,6 +207,20 @@ def test_bmm_transposed(dev, dtype):
     check_bmm(dev, 8, 256, 256, 256, dtype, "tr")
 
 
+@pytest.mark.parametrize("case", [(torch.bfloat16, 36, 2048, 2048, 64), (torch.float16, 24, 2000, 3008, 96)],
+                         ids=str)
+def test_bmm_streamed_output(dev, case):
+    """Outputs past the 256 MiB last-level cache (302 and 289 MB) leave the LDS-staged
+    epilogue through non-temporal stores: whole 256 x 256 tiles with one K stage, and a ragged
+    last tile row with a K edge (fp16)."""
+    dtype, Bb, M, N, K = case
+    g = gen(77)
+    a, b = rand((Bb, M, K), dtype, g).to(dev), rand((Bb, K, N), dtype, g).to(dev)
+    assert Bb * M * N * a.element_size() >= 256 << 20
+    got = mb.bmm(a, b)
+    assert_parity_full(got, a, b, rows=16, tag=f"bmm streamed {case}")
+
+
 @pytest.mark.parametrize("dtype", ALL, ids=str)
 @pytest.mark.parametrize("bshape", [(4, 128, 96), (4, 1, 96), (4, 128, 1), (1, 128, 96), (128, 96), (96,),
                                     (1,), ()], ids=str)
