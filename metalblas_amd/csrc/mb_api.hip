@@ -1148,13 +1148,116 @@ bool plan_peel(const mb_gemm_desc *d, Peel &pe) {
 
 constexpr uint64_t kSentBase = uint64_t(1) << 56;   // above every canonical host / HSA address
 constexpr uint64_t kSentSpan = uint64_t(1) << 52;   // one span per operand: a, b, c, bias
+// spans 4..6: the workspace copies of a packed peel (placed at run time)
+constexpr uint64_t kSentCopy = kSentBase + 4 * kSentSpan;
 
 struct CallPlan {
     int n = 0;       // launch sequences: 1, or the 2-3 parts of a peeled product
     Plan part[3];
+    int ncopy = 0;   // packed peel: operand copies made before the parts
+    PackOp copy[3];  // (their .off is the workspace offset; the parts' workspace follows)
+    int64_t copy_bytes = 0;
 };
 
-int plan_call(const mb_gemm_desc *d, CallPlan &cp) {
+// ---- packed peel ------------------------------------------------------------------------------
+// A product whose operands are both copied anyway (rows no loader can stream in place: an odd
+// K, a storage offset) and whose M or N ends 1..16 past a multiple of 256 (4097^3: 17 x 33
+// tiles of 256 x 128 in three rounds) is peeled after the copies: A and B are copied once,
+// row-major with K zero-padded to a whole stage (aligned rows), B's last 1..16 columns also
+// K-contiguous, and the core runs whole 256 x 256 tiles on the copies while the strips stream
+// them on the fast GEMV or thin kernels, all on the caller's stream: rows [M', M) x columns
+// [0, N') and all rows x columns [N', N) (the corner with the columns).  The copies take the front
+// of the workspace; the parts are planned on sentinel pointers for them (spans 4..6), which
+// gemm_impl places.  Row-major A and B (unit column stride), batch 1, bf16 / fp16, the AUTO
+// backend, no tile or split request.
+bool plan_packed_peel(const mb_gemm_desc *d, CallPlan &cp, bool sizing) {
+    if (d->backend != MB_BACKEND_AUTO || d->batch != 1 || d->split_k != 0 || d->tile[0] > 0 || d->tile[1] > 0)
+        return false;
+    if (d->dtype != MB_DTYPE_BF16 && d->dtype != MB_DTYPE_F16) return false;
+    if (d->M < 2048 || d->N < 2048 || d->K < 2048 || d->a.col_stride != 1 || d->b.col_stride != 1) return false;
+    if (d->conj_a || d->conj_b || (d->flags & kFlagStaticScratch)) return false;
+    if (!sizing && !d->workspace) return false;
+    const int64_t rm = d->M % 256, rn = d->N % 256;
+    const bool pm = rm >= 1 && rm <= 16, pn = rn >= 1 && rn <= 16;
+    if (!pm && !pn) return false;
+    Plan whole;
+    if (make_plan(d, whole) != MB_OK || whole.family != MB_FAMILY_MFMA || !whole.pack[0].on || !whole.pack[1].on)
+        return false;
+    const int es = dtype_size(d->dtype);
+    const int64_t mm = d->M - (pm ? rm : 0), nn = d->N - (pn ? rn : 0);
+    const int64_t Kp = (d->K + 128 / es - 1) / (128 / es) * (128 / es);   // whole 128-byte stages
+    const int64_t Np = (d->N + 16 / es - 1) / (16 / es) * (16 / es);      // 16-byte rows
+    auto copy_op = [&](const void *src, int64_t s_rs, int64_t s_cs, int64_t rows, int64_t cols, int64_t rows_p,
+                       int64_t cols_p, bool contig_cols, int64_t &off) {
+        PackOp pk;
+        PackArgs &a = pk.a;
+        memset(&a, 0, sizeof(a));
+        a.src = src;
+        a.s_rs = s_rs; a.s_cs = s_cs;
+        a.rows = (int)rows; a.cols = (int)cols; a.rows_p = (int)rows_p; a.cols_p = (int)cols_p;
+        a.contig_cols = contig_cols;
+        a.d_rs = contig_cols ? cols_p : 1;
+        a.d_cs = contig_cols ? 1 : rows_p;
+        a.batch = 1;
+        a.es = es;
+        pk.on = true;
+        pk.off = off;
+        off += (rows_p * cols_p * es + 255) / 256 * 256;
+        return pk;
+    };
+    int64_t off = 0;
+    cp.ncopy = 0;
+    // A: M x Kp row-major; B: Kp x Np row-major; B's columns [nn, N): K-contiguous, rn x Kp
+    cp.copy[cp.ncopy++] = copy_op(d->a.ptr, d->a.row_stride, 1, d->M, d->K, d->M, Kp, true, off);
+    cp.copy[cp.ncopy++] = copy_op(d->b.ptr, d->b.row_stride, 1, d->K, d->N, Kp, Np, true, off);
+    if (pn)
+        cp.copy[cp.ncopy++] = copy_op((const char *)d->b.ptr + nn * es, d->b.row_stride, 1, d->K, rn, Kp, rn, false, off);
+    cp.copy_bytes = off;
+    const int64_t avail = sizing ? (int64_t(1) << 50) : d->workspace_bytes - off;
+    if (avail < 0) return false;
+    auto sent = [es](int k, int64_t elems) { return (void *)(uintptr_t)(kSentCopy + (uint64_t)k * kSentSpan + elems * es); };
+    auto at = [es](void *ptr, int64_t elems) { return ptr ? (void *)((char *)ptr + elems * es) : ptr; };
+    mb_gemm_desc base = *d;
+    base.K = Kp;
+    base.a = {sent(0, 0), Kp, 1, 0};
+    base.b = {sent(1, 0), Np, 1, 0};
+    base.workspace = sizing ? (void *)(uintptr_t)1 : d->workspace;
+    base.workspace_bytes = avail;
+    mb_gemm_desc part[3];
+    int n = 0;
+    part[n] = base;
+    part[n].M = mm;
+    part[n].N = nn;
+    ++n;
+    if (pm) {   // rows [mm, M) x columns [0, nn) (8-aligned rows for the x @ W stream)
+        part[n] = base;
+        part[n].M = rm;
+        part[n].N = nn;
+        part[n].a.ptr = sent(0, mm * Kp);
+        part[n].c.ptr = at(d->c.ptr, mm * d->c.row_stride);
+        part[n].bias.ptr = at(d->bias.ptr, mm * d->bias.row_stride);
+        ++n;
+    }
+    if (pn) {   // all rows x columns [nn, N), against the K-contiguous column copy
+        part[n] = base;
+        part[n].N = rn;
+        part[n].b = {sent(2, 0), 1, Kp, 0};
+        part[n].c.ptr = at(d->c.ptr, nn * d->c.col_stride);
+        part[n].bias.ptr = at(d->bias.ptr, nn * d->bias.col_stride);
+        ++n;
+    }
+    for (int i = 0; i < n; ++i)
+        if (plan_one(&part[i], cp.part[i]) != MB_OK) return false;
+    const Plan &pc = cp.part[0];
+    if (pc.family != MB_FAMILY_MFMA || pc.tile.bm != 256 || pc.tile.bn != 256 || pc.pack[0].on || pc.pack[1].on)
+        return false;
+    for (int i = 1; i < n; ++i)
+        if (!streaming_plan(cp.part[i]) || cp.part[i].pack[0].on || cp.part[i].pack[1].on) return false;
+    cp.n = n;
+    return true;
+}
+
+int plan_call(const mb_gemm_desc *d, CallPlan &cp, bool sizing = false) {
     Peel pe;
     if (plan_peel(d, pe)) {
         cp.n = pe.n;
@@ -1164,8 +1267,24 @@ int plan_call(const mb_gemm_desc *d, CallPlan &cp) {
         }
         return MB_OK;
     }
+    {
+        CallPlan pp;
+        if (plan_packed_peel(d, pp, sizing)) {
+            cp = pp;
+            return MB_OK;
+        }
+    }
+    cp = CallPlan();
     cp.n = 1;
     return plan_one(d, cp.part[0]);
+}
+
+// the workspace a call plan needs: its copies, then the largest part's own workspace (the
+// parts run one after another)
+int64_t call_ws_bytes(const CallPlan &cp) {
+    int64_t ws = 0;
+    for (int i = 0; i < cp.n; ++i) ws = std::max<int64_t>(ws, cp.part[i].ws_bytes);
+    return cp.copy_bytes + ws;
 }
 
 // Calls f on every device pointer a plan holds (all are copies of, or offsets into, the
@@ -1242,10 +1361,13 @@ int cached_plan(const mb_gemm_desc *desc, CallPlan &cp) {
         g_cache.emplace(std::move(key), cp);
     }
     for (int i = 0; i < cp.n; ++i) each_ptr(cp.part[i], [&](auto *&p) { relocate(p, r); });
+    for (int i = 0; i < cp.ncopy; ++i) relocate(cp.copy[i].a.src, r);
     if (hit && cache_mode() == 2) {
         CallPlan fresh;
         const int st = plan_call(desc, fresh);
-        bool same = st == MB_OK && fresh.n == cp.n;
+        bool same = st == MB_OK && fresh.n == cp.n && fresh.ncopy == cp.ncopy && fresh.copy_bytes == cp.copy_bytes;
+        for (int i = 0; same && i < cp.ncopy; ++i)
+            same = fresh.copy[i].a.src == cp.copy[i].a.src && fresh.copy[i].off == cp.copy[i].off;
         for (int i = 0; same && i < cp.n; ++i) {
             Plan &x = cp.part[i], &y = fresh.part[i];
             uint64_t px[32], py[32];
@@ -1329,11 +1451,40 @@ int64_t mb_gemm_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 namespace {
 
+// a packed peel's sentinel pointer (spans 4..6) -> its place in the workspace copies
+template <class T>
+void place_copy(T *&ptr, const CallPlan &cp, char *wsb) {
+    const uint64_t v = (uint64_t)(uintptr_t)ptr;
+    if (v < kSentCopy || v >= kSentCopy + (uint64_t)cp.ncopy * kSentSpan) return;
+    const int k = (int)((v - kSentCopy) / kSentSpan);
+    ptr = (T *)(wsb + cp.copy[k].off + (v - kSentCopy - (uint64_t)k * kSentSpan));
+}
+
 int gemm_impl(const mb_gemm_desc *desc, void *stream) {
     CallPlan cp;
     const int st = cache_mode() ? cached_plan(desc, cp) : plan_call(desc, cp);
     if (st != MB_OK) return st;
     if (desc->flags & MB_FLAG_DRY_RUN) return MB_OK;
+    if (cp.ncopy > 0) {
+        // packed peel: the operand copies first, then the parts on them, each part's own
+        // workspace after the copies
+        if (!desc->workspace || desc->workspace_bytes < call_ws_bytes(cp)) return MB_ERR_WORKSPACE;
+        char *wsb = (char *)desc->workspace;
+        for (int i = 0; i < cp.ncopy; ++i) {
+            PackArgs a = cp.copy[i].a;
+            a.dst = wsb + cp.copy[i].off;
+            if (launch_pack(a, (hipStream_t)stream) != hipSuccess) return MB_ERR_LAUNCH;
+        }
+        mb_gemm_desc rest = *desc;
+        rest.workspace = wsb + cp.copy_bytes;
+        rest.workspace_bytes = desc->workspace_bytes - cp.copy_bytes;
+        for (int i = 0; i < cp.n; ++i) {
+            each_ptr(cp.part[i], [&](auto *&p) { place_copy(p, cp, wsb); });
+            const int rs = run_plan(cp.part[i], &rest, (hipStream_t)stream, nullptr);
+            if (rs != MB_OK) return rs;
+        }
+        return MB_OK;
+    }
     // the parts of a peeled product run one after another on the caller's stream and share
     // its workspace (each part's descriptor is desc with offset operands)
     for (int i = 0; i < cp.n; ++i) {
@@ -1359,6 +1510,8 @@ int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
         }
         return ws;
     }
+    CallPlan cp;
+    if (desc && plan_packed_peel(desc, cp, true)) return call_ws_bytes(cp);
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
@@ -1369,14 +1522,20 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
     if (!info) return MB_ERR_INVALID_ARG;
     Plan pl;
     Peel pe;
+    CallPlan cp;
     // a peeled product reports its core (the strips run on the GEMV / thin kernels)
     const bool peeled = desc && plan_peel(desc, pe);
-    int st = make_plan(peeled ? &pe.part[0] : desc, pl);
+    const bool packed_peel = !peeled && desc && plan_packed_peel(desc, cp, true);
+    int st = MB_OK;
+    if (packed_peel)
+        pl = cp.part[0];
+    else
+        st = make_plan(peeled ? &pe.part[0] : desc, pl);
     if (st != MB_OK) return st;
     memset(info, 0, sizeof(*info));
     info->family = pl.family;
     info->transposed = pl.p.transposed;
-    info->workspace_bytes = peeled ? mb_gemm_workspace_bytes(desc) : pl.ws_bytes;
+    info->workspace_bytes = peeled || packed_peel ? mb_gemm_workspace_bytes(desc) : pl.ws_bytes;
     info->split_k = 1;
     if (pl.family == MB_FAMILY_MFMA) {
         info->tile[0] = pl.tile.bm;
@@ -1434,8 +1593,14 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
         ++out;
     };
     emit(pl.tile);
-    // thin and deep-K products have one matrix-core tile
+    // thin and deep-K products have one matrix-core tile; a peeled product keeps its peeled plan
+    // (a tile request turns the peeling off)
     if (thin_tile(pl.tile) || pl.tile.sched == 2) return 1;
+    {
+        Peel pe;
+        CallPlan cp;
+        if (plan_peel(desc, pe) || plan_packed_peel(desc, cp, true)) return 1;
+    }
     for (int i = 0; i < n && i < 32; ++i) {
         const MfmaTile &t = list[i];
         if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn &&

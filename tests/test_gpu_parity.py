@@ -661,6 +661,31 @@ def test_peeled_edges(dev, case):
         assert_parity(got[:, nn:], a, b[:, nn:], tag=f"peel {case} columns", **kw)
 
 
+@pytest.mark.parametrize("case", [("bf16", 4097, 4097, 4097, None, 0), ("fp16", 4096, 4100, 4099, "row", 0),
+                                  ("bf16", 4100, 4096, 4097, None, 1), ("bf16", 4097, 4097, 4097, "full", 0)],
+                         ids=str)
+def test_packed_peel(dev, case):
+    """Products whose operands are both copied (odd K, a column-sliced B) and whose M or N ends
+    1..16 past a multiple of 256: A and B are copied first (K zero-padded to a stage, B's last
+    columns also K-contiguous), then the core runs whole 256 x 256 tiles on the copies and the
+    strips the streaming GEMV.  Every element is checked (the oracle on spread rows pins a
+    float64 product of the whole output)."""
+    name, M, N, K, bias_kind, b_slice = case
+    dtype = {"bf16": torch.bfloat16, "fp16": torch.float16}[name]
+    g = gen(M + N + K)
+    a = rand((M, K), dtype, g).to(dev)
+    b = rand((K, N + b_slice), dtype, g).to(dev)[:, :N]
+    info = mb.kernels.plan(a, b)
+    assert info["tile"][:2] == (256, 256) and info["grid"][0] == 256, info
+    if bias_kind is None:
+        got = mb.matmul(a, b)
+        assert_parity_full(got, a, b, rows=16, tag=f"packed peel {case}")
+    else:
+        bias = rand((M, N) if bias_kind == "full" else (N,), dtype, g).to(dev)
+        got = mb.addmm(bias, a, b, beta=0.5, alpha=2.0)
+        assert_parity_full(got, a, b, bias=bias, beta=0.5, alpha=2.0, rows=16, tag=f"packed peel {case}")
+
+
 # ---- small generic tiles (16 x 16 / 32 x 32, no K slices) -------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.int16, torch.int32, torch.int64], ids=str)

@@ -226,12 +226,37 @@ def test_plan_thin_problems_fill_two_workgroups_per_cu():
 
 
 def test_plan_both_operands_copied_pad_k_to_a_stage():
-    # 4097^3 bf16: both operands are copied (odd leading dimensions); K is zero-padded to 4160
-    # (a whole 64-deep stage) in both copies: A 4097 x 4160, B 4160 x 4104
+    # 4128 x 4128 x 4097 bf16: both operands are copied (odd leading dimensions, B a column
+    # slice with row stride 4129); K is zero-padded to 4160 (a whole 64-deep stage) in both
+    # copies: A 4128 x 4160, B 4160 x 4128
+    a = torch.empty(4128, 4097, dtype=torch.bfloat16)
+    b = torch.empty(4097, 4129, dtype=torch.bfloat16)[:, :4128]
+    p = _plan(torch.bfloat16, a, b)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k == 1
+    assert p.workspace_bytes == 4128 * 4160 * 2 + 4160 * 4128 * 2
+
+
+def test_plan_packed_peel():
+    # 4097^3 bf16: both operands are copied anyway, so they are copied first (A 4097 x 4160, B
+    # 4160 x 4104, B's last column K-contiguous 1 x 4160) and the product is peeled on the
+    # copies: the plan reports the 4096^2 core on 256 whole 256 x 256 tiles; the workspace holds
+    # the copies and then the largest part's own need; the tuner gets one candidate (a tile
+    # request would turn the peeling off)
     a = torch.empty(4097, 4097, dtype=torch.bfloat16)
     p = _plan(torch.bfloat16, a, a)
-    assert _lib.FAMILY_NAMES[p.family] == "mfma" and p.split_k == 1
-    assert p.workspace_bytes == (4097 * 4160 * 2 + 255) // 256 * 256 + 4160 * 4104 * 2
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile)[:2] == (256, 256)
+    assert tuple(p.grid) == (256, 1, 1) and p.split_k == 1
+    copies = (4097 * 4160 * 2 + 255) // 256 * 256 + 4160 * 4104 * 2 + (4160 * 2 + 255) // 256 * 256
+    assert copies <= p.workspace_bytes <= copies + (8 << 20)
+    d = _desc(torch.bfloat16, a, a)
+    assert _lib.load().mb_gemm_workspace_bytes(ctypes.byref(d)) == p.workspace_bytes
+    assert len(_lib.tile_candidates(d)) == 1
+    # an explicit tile keeps the whole product (561 tiles of 256 x 128)
+    p = _plan(torch.bfloat16, a, a, tile=(256, 128, 64, 2, 4, 2))
+    assert tuple(p.tile)[:2] == (256, 128) and tuple(p.grid) == (561, 1, 1)
+    # a core too small for 256 whole tiles stays one product
+    a2, b2 = torch.empty(2056, 2051, dtype=torch.bfloat16), torch.empty(2051, 4100, dtype=torch.bfloat16)
+    assert tuple(_plan(torch.bfloat16, a2, b2).tile)[:2] != (256, 256)
 
 
 def test_plan_peels_a_thin_edge_off_whole_tiles():
@@ -245,14 +270,11 @@ def test_plan_peels_a_thin_edge_off_whole_tiles():
     assert tuple(p.grid) == (256, 1, 1)
     d = _desc(torch.bfloat16, a, b)
     assert _lib.load().mb_gemm_workspace_bytes(ctypes.byref(d)) == p.workspace_bytes > 0
-    # not peeled: a remainder above 16 rows, an explicit tile, or strips without a streaming
-    # kernel (4097^3: every row of both operands is misaligned)
+    # not peeled: a remainder above 16 rows, or an explicit tile
     a2 = torch.empty(4128, 4096, dtype=torch.bfloat16)
     assert tuple(_plan(torch.bfloat16, a2, b).grid) != (256, 1, 1)
     p = _plan(torch.bfloat16, a, b, tile=(256, 128, 64, 2, 4, 2))
     assert tuple(p.tile)[:2] == (256, 128)
-    a3 = torch.empty(4097, 4097, dtype=torch.bfloat16)
-    assert tuple(_plan(torch.bfloat16, a3, a3).grid) == (561, 1, 1)
 
 
 def test_plan_config4_splitk_and_batches():

@@ -59,6 +59,9 @@ run("peel M", bf, 1, 4097, 4096, 4096, rm(4097, 4096), rm(4096, 4096), rm(4097, 
 run("peel N", bf, 1, 4096, 4100, 4096, rm(4096, 4096), rm(4096, 4100), rm(4096, 4100))
 run("peel both + addmm", f16, 1, 4097, 4100, 2048, rm(4097, 2048), rm(2048, 4100), rm(4097, 4100),
     bias=(0, 1, 0), epilogue=ep)
+run("packed peel 4097^3", bf, 1, 4097, 4097, 4097, rm(4097, 4097), rm(4097, 4097), rm(4097, 4097))
+run("packed peel N + addmm", f16, 1, 4096, 4100, 4100, rm(4096, 4100), rm(4100, 4100), rm(4096, 4100),
+    bias=(0, 1, 0), epilogue=ep)
 run("addmm bias row", bf, 1, 2048, 2048, 4096, rm(2048, 4096), rm(4096, 2048), rm(2048, 2048),
     bias=(0, 1, 0), epilogue=ep)
 run("split-K 128x128x65536", f16, 1, 128, 128, 65536, rm(128, 65536), rm(65536, 128), rm(128, 128))
