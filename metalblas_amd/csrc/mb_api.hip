@@ -750,9 +750,10 @@ bool plan_complex(const Prob &p, Plan &pl) {
     return true;
 }
 
-// Products with a few vectors (2..16) and a large matrix run on the matrix cores, which read
-// the matrix once at HBM speed whatever the vector count (the VALU GEMV kernels spend nv FMAs
-// per matrix element, which outgrows the HBM stream from about 4 vectors up).  Thin tiles:
+// Products with a few vectors (up to 32; one only against a mid-size N-contiguous matrix) and a
+// large matrix run on the matrix cores, which read the matrix once at HBM speed whatever the
+// vector count (the VALU GEMV kernels spend nv FMAs per matrix element, which outgrows the HBM
+// stream from about 4 vectors up).  Thin tiles:
 //   4 x 8    (k_dotx):     matrix = A, K-contiguous; up to 8 vectors = columns of B, whole K;
 //   4 x 16   (k_thin_dot4) and 64 x 16 (k_thin_dot): matrix = A, K-contiguous, K slices;
 //   32 x 256 (k_thin16):   matrix = B, N-contiguous; vectors = rows of A.
@@ -763,7 +764,7 @@ bool plan_complex(const Prob &p, Plan &pl) {
 // Measured on MI355X (bf16, 16384^2 matrix): the 32 x 256 tile streams at ~92 us for every
 // vector count from 2 up (VALU: 95 us at 2 vectors, 118 at 8, 189 at 16); k_thin_dot4 at
 // ~111 us (VALU: 95-97 us at 2 and 4 vectors, 347 at 3, 195 at 8, 624 at 16).
-constexpr int kThinMfmaMinNvRows = 2, kThinMfmaMinNvDot = 5;
+constexpr int kThinMfmaMinNvDot = 5;
 
 bool plan_thin_mfma(const Prob &p, Plan &pl) {
     if (p.dt != MB_DTYPE_BF16 && p.dt != MB_DTYPE_F16) return false;
@@ -785,7 +786,14 @@ bool plan_thin_mfma(const Prob &p, Plan &pl) {
             // ~111 us); 3 vectors have no fast VALU form (347 us)
             if (nv < kThinMfmaMinNvDot && nv != 3) return false;
         } else {
-            if (nv < kThinMfmaMinNvRows) return false;
+            // one vector (x @ W): the tile's stream needs no K-slice planes when the columns
+            // fill the CUs, and wins below ~0.4 GB of matrix; above it the VALU stream's longer
+            // runs win.  Measured on MI355X (bf16, us, VALU -> thin tile): 4096^2 19.0 -> 11.9,
+            // 32000 x 4096 46.4 -> 43.8, 65536 x 2048 45.5 -> 42.4; kept: 16384^2 82.0 (85.4),
+            // 32000 x 8192 82.4 (84.8).
+            const int64_t mat1 = wide * p.K * p.batch * dtype_size(p.dt);
+            if (nv == 1 && (mat1 < (32LL << 20) || mat1 >= (384LL << 20) || (wide + 255) / 256 * p.batch < 8))
+                return false;
             // N-contiguous matrix on the 32 x 256 tile.  Up to 16 vectors: a large matrix
             // (>= 32 MiB over >= 8 tiles), also with a short K or a batch, where the VALU
             // kernel's K slices write fp32 planes of nv x N per slice.  17-32 vectors (where

@@ -207,12 +207,12 @@ def test_bmm_transposed(dev, dtype):
     check_bmm(dev, 8, 256, 256, 256, dtype, "tr")
 
 
-@pytest.mark.parametrize("case", [(torch.bfloat16, 36, 2048, 2048, 64), (torch.float16, 24, 2000, 3008, 96)],
-                         ids=str)
+@pytest.mark.parametrize("case", [(torch.bfloat16, 36, 2048, 2048, 64), (torch.float16, 24, 2000, 3008, 96),
+                                  (torch.int8, 17, 4096, 4096, 128)], ids=str)
 def test_bmm_streamed_output(dev, case):
-    """Outputs past the 256 MiB last-level cache (302 and 289 MB) leave the LDS-staged
-    epilogue through non-temporal stores: whole 256 x 256 tiles with one K stage, and a ragged
-    last tile row with a K edge (fp16)."""
+    """Outputs past the 256 MiB last-level cache (302, 289 and 285 MB) leave the LDS-staged
+    epilogue through non-temporal stores: whole 256 x 256 tiles with one K stage, a ragged last
+    tile row with a K edge (fp16), and 8-bit outputs (16 per chunk, bit-exact)."""
     dtype, Bb, M, N, K = case
     g = gen(77)
     a, b = rand((Bb, M, K), dtype, g).to(dev), rand((Bb, K, N), dtype, g).to(dev)
@@ -442,6 +442,7 @@ def test_thin_matrix_cores_more(dev, case):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=str)
 @pytest.mark.parametrize("case", [(16, 16, 2048, 512, None), (64, 24, 1024, 256, None), (256, 16, 1024, 64, None),
                                   (128, 16, 1024, 1024, None), (1, 16, 16384, 1024, None),
+                                  (1, 1, 16384, 2048, None), (1, 1, 4096, 4096, None),
                                   (1, 32, 2304, 520, (32, 256)), (1, 16, 1024, 40, (32, 256)),
                                   (1, 5, 1000, 136, (32, 256)), (1, 32, 2304, 520, (32, 128)),
                                   (1, 16, 1024, 40, (32, 128)), (1, 5, 1000, 136, (32, 128))], ids=str)

@@ -207,9 +207,17 @@ def test_plan_config2_gemv_families():
 
 
 def test_plan_narrow_x_at_w_fills_the_cus():
-    # 4096 columns: two 2048-column bands (no band overhangs the rows), K slices of 32 rows
+    # x @ W with 4096 columns: the thin matrix-core tile 32 x 128 over 8 K slices (32 tiles x 8
+    # = 256 workgroups); a 0.5 GB matrix stays on the VALU stream
     W = torch.empty(4096, 4096, dtype=torch.bfloat16)
-    p = _plan(torch.bfloat16, torch.empty(1, 4096, dtype=torch.bfloat16), W)
+    x = torch.empty(1, 4096, dtype=torch.bfloat16)
+    p = _plan(torch.bfloat16, x, W)
+    assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == (32, 128) and p.split_k == 8
+    big = _plan(torch.bfloat16, torch.empty(1, 16384, dtype=torch.bfloat16), torch.empty(16384, 16384, dtype=torch.bfloat16))
+    assert _lib.FAMILY_NAMES[big.family] == "gemv_axpy"
+    # the VALU stream on request: two 2048-column bands (no band overhangs the rows), K slices
+    # of 32 rows
+    p = _plan(torch.bfloat16, x, W, backend=_lib.BACKEND_GEMV)
     assert _lib.FAMILY_NAMES[p.family] == "gemv_axpy"
     assert p.split_k == 128 and p.workspace_bytes == 128 * 4096 * 4
 
