@@ -1,8 +1,9 @@
-// Thin products on the matrix cores, bf16_t / f16_t: a handful of vectors (<= 16) against a
-// large matrix that is streamed from HBM exactly once.
+// Thin products on the matrix cores, bf16_t / f16_t: a handful of vectors against a large
+// matrix that is streamed from HBM exactly once.
 //
-//   * k_thin16 (mfma16.hpp), tile 32 x 256: the vectors are the rows of A (K-contiguous), the
-//     matrix B is N-contiguous; B goes through a 4-deep LDS-direct ring (512-byte row spans).
+//   * k_thin16 (mfma16.hpp), tile 32 x 256 or 32 x 128: the vectors (up to 32) are the rows of
+//     A (K-contiguous), the matrix B is N-contiguous; B goes through a 4-deep LDS-direct ring
+//     (512- or 256-byte row spans).
 //   * k_thin_dot (below), tile 64 x 16: the matrix A is K-contiguous and the vectors are the
 //     columns of B (K-contiguous).  The matrix never touches LDS: each wave loads 1 KiB of
 //     each of its 16 rows per 512-deep macro step straight into the registers that feed

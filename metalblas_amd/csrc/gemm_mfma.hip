@@ -42,8 +42,9 @@ constexpr TileEntry kTiles16[] = {
     {256, 256, 2, 4, 1}, {256, 128, 2, 4, 1}, {256, 256, 2, 2, 0}, {256, 256, 2, 4, 0}, {256, 128, 2, 2, 0}, {128, 256, 2, 2, 0},
     {128, 128, 2, 2, 0}, {128, 64, 2, 2, 0},  {64, 128, 2, 2, 0},  {64, 64, 2, 2, 0},  {32, 32, 1, 1, 0},
     // thin tiles for products with a few vectors (bf16 / fp16): k_thin_dot 64 x 16 and
-    // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 (A K-contiguous, B
-    // N-contiguous), k_dotx 4 x 8 (A K-contiguous, up to 16 waves over the whole K)
+    // k_thin_dot4 4 x 16 (A and B K-contiguous), k_thin16 32 x 256 and 32 x 128 (A
+    // K-contiguous, B N-contiguous), k_dotx 4 x 8 (A K-contiguous, up to 16 waves over the
+    // whole K)
     {64, 16, 4, 1, 0},   {32, 256, 1, 4, 0},  {32, 128, 1, 4, 0}, {4, 16, 1, 1, 0},  {4, 8, 16, 1, 0},
     // the deep-K schedule of the 64 x 64 tile (bf16 / fp16): few output tiles, many K slices
     {64, 64, 2, 2, 2},

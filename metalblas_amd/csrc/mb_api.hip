@@ -349,7 +349,7 @@ MfmaTile snap_tile(int dt, const int32_t *t, bool a_kc, bool b_kc, bool thin_ok)
     double bestd = 1e30;
     for (int i = 0; i < n && i < 32; ++i) {
         // thin tiles: bf16 / fp16, 64 x 16 and 4 x 16 with both operands K-contiguous, 4 x 8
-        // with A K-contiguous, 32 x 256 with A K-contiguous and B N-contiguous
+        // with A K-contiguous, 32 x 256 / 32 x 128 with A K-contiguous and B N-contiguous
         if (thin_tile(list[i]) &&
             (!thin_ok || (dt != MB_DTYPE_BF16 && dt != MB_DTYPE_F16) ||
              (list[i].bn == 16 ? !(a_kc && b_kc) : list[i].bn == 8 ? !a_kc : !(a_kc && !b_kc))))
@@ -756,10 +756,10 @@ bool plan_complex(const Prob &p, Plan &pl) {
 // stream from about 4 vectors up).  Thin tiles:
 //   4 x 8    (k_dotx):     matrix = A, K-contiguous; up to 8 vectors = columns of B, whole K;
 //   4 x 16   (k_thin_dot4) and 64 x 16 (k_thin_dot): matrix = A, K-contiguous, K slices;
-//   32 x 256 (k_thin16):   matrix = B, N-contiguous; vectors = rows of A.
+//   32 x 256, 32 x 128 (k_thin16): matrix = B, N-contiguous; vectors = rows of A.
 // The other two layouts are the transposed problem of these.  The vectors must be
 // K-contiguous and are copied (nv x K elements) when they are not; a matrix the loaders cannot
-// stream in place is left to the GEMV path.  K is split so that one workgroup runs per CU.
+// stream in place is left to the GEMV path.  K is split when the tiles alone leave CUs idle.
 // bf16 / fp16 only.
 // Measured on MI355X (bf16, 16384^2 matrix): the 32 x 256 tile streams at ~92 us for every
 // vector count from 2 up (VALU: 95 us at 2 vectors, 118 at 8, 189 at 16); k_thin_dot4 at

@@ -930,10 +930,10 @@ __global__ __launch_bounds__(64 * WM * WN) void k_thin16(GemmArgs g) {
     }
 }
 
-// The thin tile 32 x 256: the vectors are the rows of A (K-contiguous), the matrix B is
-// N-contiguous and streamed once with non-temporal loads (MI355X, 8 x 16384 @ 16384^2 bf16,
-// 4 K slices: 82.1 us against 88.1 us with cached loads).  4 buffers of 36 KiB: one workgroup
-// per CU.
+// The thin tiles 32 x 256 and 32 x 128: the vectors are the rows of A (K-contiguous), the
+// matrix B is N-contiguous and streamed once with non-temporal loads (MI355X, 8 x 16384 @
+// 16384^2 bf16, 4 K slices: 82.1 us against 88.1 us with cached loads).  4 buffers of 36 KiB
+// (one workgroup per CU) or of 20 KiB (two).
 template <class T, bool KTAIL>
 hipError_t launch_thin16(const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hipStream_t st) {
     if (!(t.bm == 32 && (t.bn == 256 || t.bn == 128) && t.wm == 1 && t.wn == 4 && a_kc && !b_kc))
