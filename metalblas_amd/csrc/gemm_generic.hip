@@ -371,10 +371,8 @@ hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st) {
 
 hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st) {
     const int64_t plane = (int64_t)g.batch * g.M * g.N;
-    // threads per output: at most 4 planes per thread, so each thread's loads go out as one
-    // batch (the reduction is latency bound: 8 MiB of x @ W planes in 4.5 us with two batches)
-    int tpo = 1;
-    while (tpo < 64 && (int64_t)tpo * 4 < g.splits) tpo *= 2;
+    // threads per output: enough that a block covers ~8 planes per thread
+    const int tpo = g.splits >= 128 ? 16 : g.splits >= 64 ? 8 : (g.splits >= 16 ? 4 : (g.splits >= 4 ? 2 : 1));
     const int64_t opb = 256 / tpo;
     int64_t blocks = (plane + opb - 1) / opb;
     if (blocks > 8192) blocks = 8192;
@@ -384,8 +382,6 @@ hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st) {
                 int64_t b4 = (plane / 4 + opb - 1) / opb;
                 if (b4 > 8192) b4 = 8192;
                 switch (tpo) {
-                    case 64: hipLaunchKernelGGL((k_splitk_reduce4<T, 64>), dim3(b4), dim3(256), 0, st, g); break;
-                    case 32: hipLaunchKernelGGL((k_splitk_reduce4<T, 32>), dim3(b4), dim3(256), 0, st, g); break;
                     case 16: hipLaunchKernelGGL((k_splitk_reduce4<T, 16>), dim3(b4), dim3(256), 0, st, g); break;
                     case 8: hipLaunchKernelGGL((k_splitk_reduce4<T, 8>), dim3(b4), dim3(256), 0, st, g); break;
                     case 4: hipLaunchKernelGGL((k_splitk_reduce4<T, 4>), dim3(b4), dim3(256), 0, st, g); break;
@@ -396,8 +392,6 @@ hipError_t launch_splitk_reduce(int dt, const GemmArgs &g, hipStream_t st) {
             }
         }
         switch (tpo) {
-            case 64: hipLaunchKernelGGL((k_splitk_reduce<T, 64>), dim3(blocks), dim3(256), 0, st, g); break;
-            case 32: hipLaunchKernelGGL((k_splitk_reduce<T, 32>), dim3(blocks), dim3(256), 0, st, g); break;
             case 16: hipLaunchKernelGGL((k_splitk_reduce<T, 16>), dim3(blocks), dim3(256), 0, st, g); break;
             case 8: hipLaunchKernelGGL((k_splitk_reduce<T, 8>), dim3(blocks), dim3(256), 0, st, g); break;
             case 4: hipLaunchKernelGGL((k_splitk_reduce<T, 4>), dim3(blocks), dim3(256), 0, st, g); break;
