@@ -175,7 +175,7 @@ def group_headline(torch, mb, n=8192):
 
 def group_gemv(torch, mb, n=16384):
     """Config 2: bf16 W 16384 x 16384 row-major; W@x (the reference's gemv_nt), x@W (gemv_t),
-    X(8 x K)@W (8 rows of x), W@X(K x 8)."""
+    W^T@x (the transposed-W case), X(8 x K)@W (8 rows of x), W@X(K x 8)."""
     g = _gen(torch, 1)
     Wc = torch.randn(n, n, generator=g).to(torch.bfloat16)
     xc = torch.randn(n, generator=g).to(torch.bfloat16)
@@ -184,6 +184,7 @@ def group_gemv(torch, mb, n=16384):
     W, x, X8, Xn = Wc.cuda(), xc.cuda(), X8c.cuda(), Xnc.cuda()
     y = torch.empty(n, dtype=torch.bfloat16, device="cuda")
     y2 = torch.empty(n, dtype=torch.bfloat16, device="cuda")
+    y3 = torch.empty(n, dtype=torch.bfloat16, device="cuda")
     Y8 = torch.empty(8, n, dtype=torch.bfloat16, device="cuda")
     Yn = torch.empty(n, 8, dtype=torch.bfloat16, device="cuda")
     one = 2.0 * (n * n + 2 * n)
@@ -195,6 +196,11 @@ def group_gemv(torch, mb, n=16384):
         Workload("gemv_x@W", "2", lambda: mb.matmul(x, W, out=y2),
                  (lambda o: o.reshape(1, n), x.reshape(1, n), W, {}),
                  flops=2.0 * n * n, nbytes=one, bound="hbm", cpu=lambda: torch.matmul(xc, Wc)),
+        # W^T @ x on the same row-major W (BASELINE's "transposed-W" variant): the matrix is
+        # read down its columns, so it streams like x @ W
+        Workload("gemv_Wt@x", "2", lambda: mb.matmul(W.t(), x, out=y3),
+                 (lambda o: o.reshape(n, 1), W.t(), x.reshape(n, 1), {}),
+                 flops=2.0 * n * n, nbytes=one, bound="hbm", cpu=lambda: torch.matmul(Wc.t(), xc)),
         Workload("gemv_X8@W", "2", lambda: mb.matmul(X8, W, out=Y8), (_plain, X8, W, {}),
                  flops=16.0 * n * n, nbytes=eight, bound="hbm", cpu=lambda: torch.matmul(X8c, Wc)),
         Workload("gemv_W@X8", "2", lambda: mb.matmul(W, Xn, out=Yn), (_plain, W, Xn, {}),
@@ -343,7 +349,7 @@ GROUPS = {
 # workload name -> group (for tests and --only)
 WORKLOADS = {
     "headline": ["bf16_gemm_8192"],
-    "gemv": ["gemv_W@x", "gemv_x@W", "gemv_X8@W", "gemv_W@X8"],
+    "gemv": ["gemv_W@x", "gemv_x@W", "gemv_Wt@x", "gemv_X8@W", "gemv_W@X8"],
     "layouts": [f"bf16_2048x4096x2048_{v}" for v in
                 ("rm_rm", "rm_cm", "cm_rm", "cm_cm", "row_sliced", "col_sliced", "offset17", "addmm")],
     "bmm": ["f16_bmm_8x512x512x256", "f16_bmm_broadcastB", "f16_splitk_128x128x65536"],
@@ -356,29 +362,26 @@ WORKLOADS = {
 # pricing
 # ---------------------------------------------------------------------------------------------
 
+def _sig(x, digits=4):
+    """x rounded to `digits` significant digits (keeps the JSON line short)."""
+    return float(f"{x:.{digits}g}")
+
+
 def price(w, ms):
-    """The JSON entry of one timed workload."""
-    d = {"ms": round(ms, 5), "config": w.cfg}
+    """The JSON entry of one timed workload (compact: the driver keeps the last 8 KB of the
+    line; the parity test of each entry is tests/test_gpu_configs.py::test_config[<name>])."""
+    d = {"cfg": w.cfg, "ms": _sig(ms, 5)}
     if w.bound == "hbm":
         gbs = w.nbytes / (ms * 1e-3) / 1e9
-        d.update(value=round(gbs, 1), unit="GB/s",
-                 roofline={"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                           "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes": int(w.nbytes)})
-        if w.peak_key:
-            d["tflops"] = round(w.flops / (ms * 1e-3) / 1e12, 2)
+        d["roofline"] = {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(gbs / PEAK_HBM_GBS, 4)}
     elif w.bound == "mfma":
         tf = w.flops / (ms * 1e-3) / 1e12
         unit = "TOP/s" if w.peak_key == "i8" else "TFLOP/s"
-        d.update(value=round(tf, 2), unit=unit,
-                 roofline={"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK[w.peak_key], "unit": unit,
-                           "frac": round(tf / PEAK[w.peak_key], 4),
-                           "algorithmic_flops": w.flops})
+        d["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": PEAK[w.peak_key], "unit": unit,
+                         "frac": round(tf / PEAK[w.peak_key], 4)}
     else:
-        d.update(us=round(ms * 1e3, 2), value=round(w.flops / (ms * 1e-3) / 1e9, 1), unit="GOP/s",
-                 roofline={"bound": "launch"})
-    if w.note:
-        d["roofline"]["note"] = w.note
-    d["parity_test"] = f"tests/test_gpu_configs.py::test_config[{w.name}]"
+        d["roofline"] = {"bound": "launch", "achieved": round(w.flops / (ms * 1e-3) / 1e9, 1), "unit": "GOP/s"}
     return d
 
 
@@ -417,14 +420,15 @@ def time_cpu(fn, min_runs=3, min_s=1.0):
 def cpu_entry(w, threads):
     s, runs = time_cpu(w.cpu)
     sec = s / w.cpu_frac     # seconds the whole workload would take at this rate
-    d = {"ms": round(sec * 1e3, 3), "cores": threads, "runs": runs, "sample": w.cpu_sample}
     if w.bound == "hbm":
-        d.update(value=round(w.nbytes / sec / 1e9, 2), unit="GB/s")
+        d = {"value": _sig(w.nbytes / sec / 1e9), "unit": "GB/s"}
     elif w.bound == "mfma":
-        d.update(value=round(w.flops / sec / 1e12, 4), unit="TOP/s" if w.peak_key == "i8" else "TFLOP/s")
+        d = {"value": _sig(w.flops / sec / 1e12), "unit": "TOP/s" if w.peak_key == "i8" else "TFLOP/s"}
     else:
-        d.update(value=round(w.flops / sec / 1e9, 2), unit="GOP/s")
-    return d
+        d = {"value": _sig(w.flops / sec / 1e9), "unit": "GOP/s"}
+    if w.cpu_frac != 1.0:
+        d["sample"] = w.cpu_sample
+    return d, runs
 
 
 def run_group(torch, mb, name, args, results, want, threads, headline_n):
@@ -441,7 +445,9 @@ def run_group(torch, mb, name, args, results, want, threads, headline_n):
             ms = time_events(torch, w.call, args.steps, args.warmup, CFG_WARM_MS, args.calls)
         entry = price(w, ms)
         if not args.no_cpu and w.cpu is not None:
-            entry["cpu_baseline"] = cpu_entry(w, threads)
+            entry["cpu_baseline"], runs = cpu_entry(w, threads)
+            if name == "headline":
+                entry["cpu_runs"] = runs
         results[w.name] = (w, entry)
     del ws
     torch.cuda.empty_cache()
@@ -518,29 +524,34 @@ def main(argv=None):
             "avg_launch_ms": round(ms, 4),
         }
         result["plan"] = {k: plan[k] for k in ("family", "tile", "split_k", "grid")}
-        result["parity_test"] = e["parity_test"]
         if "cpu_baseline" in e:
             c = e["cpu_baseline"]
             result["cpu_baseline"] = {"value": c["value"], "unit": c["unit"], "cores": threads,
                                       "kind": "torch.matmul", "model": cpu_model(),
-                                      "host_cpus": os.cpu_count(), "runs": c["runs"],
+                                      "host_cpus": os.cpu_count(), "runs": e["cpu_runs"],
                                       "sample": f"torch.matmul bf16 on the host CPU, {c['sample']}, "
                                                 "1 warmup + best of >= 3 runs and >= 1 s"}
     if results:
-        cfg = {name: e for name, (w, e) in results.items()}
-        for name, e in cfg.items():
-            e["roofline"]["traffic"] = TRAFFIC.get(name)
+        cfg = {}
+        for name, (w, e) in results.items():
+            e["roofline"]["traffic"] = _sig(TRAFFIC[name]) if name in TRAFFIC else None
+            cfg[name] = e
         result["configs"] = cfg
-        result["configs_timing"] = (f"each config: {args.warmup} warmup calls, {CFG_WARM_MS:g} ms of untimed "
-                                    f"calls, then {args.calls or max(args.steps, CFG_MIN_CALLS)} timed calls (HIP events)")
+        result["configs_note"] = (
+            f"each config: {args.warmup} warmup calls, {CFG_WARM_MS:g} ms of untimed calls, then "
+            f"{args.calls or max(args.steps, CFG_MIN_CALLS)} timed calls (HIP events); roofline.traffic = "
+            "HBM bytes per launch of the dominant kernel (rocprofv3 FETCH_SIZE/WRITE_SIZE, profiles/); "
+            "cpu_baseline = torch.matmul/addmm/bmm on the host CPU "
+            f"({threads} threads, best of >= 3 runs and >= 1 s) over the whole workload unless a sample "
+            "is named; parity: tests/test_gpu_configs.py::test_config[<name>]")
         if result["value"] is None:
             first = next(iter(cfg.values()))
-            result.update({"value": first["value"], "unit": first["unit"], "ms_per_step": first["ms"],
-                           "roofline": dict(first["roofline"])})
+            result.update({"value": first["roofline"]["achieved"], "unit": first["roofline"]["unit"],
+                           "ms_per_step": first["ms"], "roofline": dict(first["roofline"])})
     if not args.no_cpu and "cpu_baseline" not in result and results:
         result["cpu_baseline"] = {"cores": threads, "kind": "torch.matmul", "model": cpu_model(),
                                   "note": "per config, under configs.<name>.cpu_baseline"}
-    print(json.dumps(result))
+    print(json.dumps(result, separators=(",", ":")))
 
 
 if __name__ == "__main__":

@@ -14,7 +14,9 @@
  *   - Scratch space (split-K partial planes) is provided by the caller: query the size with
  *     mb_gemm_workspace_bytes() for the same descriptor and pass it in desc->workspace.
  *   - Return value 0 = success, negative = mb_status (see mb_strerror()).
- *   - Thread-safe: no mutable global state besides a per-process device-property cache.
+ *   - Thread-safe.  Mutable global state, each guarded by a mutex: the per-process
+ *     device-property cache, the plan cache of mb_gemm() (up to 1024 call signatures), and the
+ *     per-device address table of mb_gemm_noalloc()'s static scratch buffer.
  *
  * Reference interfaces this ABI replaces (Isalia20/metalBLAS, file:line):
  *   - the Metal kernel handles assembled by metalblas/kernels.py:76-253 and launched as
@@ -154,11 +156,15 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream);
  * expansions a product needs run in a static per-device buffer of
  * mb_gemm_noalloc_scratch_bytes() bytes (64 MiB, enough for every BASELINE workload) that the
  * library holds on each device it runs on until the process ends; desc->workspace and
- * desc->workspace_bytes are ignored.  The same plan and kernels as mb_gemm() with a workspace
- * run, so results are identical.  A product that needs more scratch than the buffer holds
- * returns MB_ERR_SCRATCH_LIMIT and queues nothing.  Calls share the device's buffer: calls that
+ * desc->workspace_bytes are ignored.  The plan is the one mb_gemm() runs with a workspace of
+ * mb_gemm_noalloc_scratch_bytes() bytes: the same kernels, hence identical results, for every
+ * product whose full plan fits the buffer (mb_gemm_workspace_bytes() <= that size), edge-peeled
+ * products included.  A product whose peeled plan would not fit runs unpeeled if that fits;
+ * one that needs more scratch than the buffer holds either way returns MB_ERR_SCRATCH_LIMIT and
+ * queues nothing.  Calls share the device's buffer: calls that
  * overlap on one device (different streams or host threads) race; calls queued on one stream
- * are ordered and safe.  desc->flags may be 0 or MB_FLAG_DRY_RUN. */
+ * are ordered and safe.  desc->flags may be 0 or MB_FLAG_DRY_RUN (every entry point rejects
+ * other bits with MB_ERR_INVALID_ARG). */
 int mb_gemm_noalloc(const mb_gemm_desc *desc, void *stream);
 
 /* Size of mb_gemm_noalloc's static per-device scratch buffer, in bytes. */

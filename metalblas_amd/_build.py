@@ -12,6 +12,7 @@ import concurrent.futures as _cf
 import os
 import shutil
 import subprocess
+import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
@@ -90,7 +91,12 @@ def _compile(args):
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> str:
-    """Compile every csrc/*.hip for gfx950 and link libmetalblas_hip.so (always rebuilds)."""
+    """Compile every csrc/*.hip for gfx950 and link libmetalblas_hip.so (always rebuilds).
+
+    The core library is linked first.  The optional compiled fast path (``_fast``) is built
+    after it; if its compile or link fails (missing torch or Python headers, an ABI mismatch)
+    the failure is reported as a warning, any stale ``_fast`` module is removed so it cannot
+    bind an older ABI, and the Python path keeps working on the core library alone."""
     hipcc = _hipcc()
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
@@ -100,23 +106,32 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         fast = ex.submit(_compile_fast, fast_obj)
         list(ex.map(_compile, [(hipcc, s, o) for s, o in zip(srcs, objs)]))
-        fast.result()
+        fast_err = fast.exception()
     out_tmp = LIB_PATH + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", out_tmp, *objs]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr[-6000:]}")
     os.replace(out_tmp, LIB_PATH)
-    target = _fast_target()
-    _, ldflags = _fast_flags()
-    cmd = [os.environ.get("CXX", "g++"), "-shared", "-o", target + ".tmp", fast_obj, *ldflags]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"link of the fast path failed:\n{proc.stderr[-6000:]}")
-    os.replace(target + ".tmp", target)
     if verbose:
         print(f"built {LIB_PATH}")
-        print(f"built {target}")
+    target = _fast_target()
+    if fast_err is None:
+        _, ldflags = _fast_flags()
+        cmd = [os.environ.get("CXX", "g++"), "-shared", "-o", target + ".tmp", fast_obj, *ldflags]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            fast_err = RuntimeError(f"link of the fast path failed:\n{proc.stderr[-6000:]}")
+        else:
+            os.replace(target + ".tmp", target)
+            if verbose:
+                print(f"built {target}")
+    if fast_err is not None:
+        for stale in (target, target + ".tmp"):
+            if os.path.exists(stale):
+                os.remove(stale)
+        print(f"warning: metalblas_amd fast path not built ({fast_err}); the Python path runs "
+              "on the core library", file=sys.stderr)
     return LIB_PATH
 
 

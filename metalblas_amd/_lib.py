@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import threading
 
 import torch
 
@@ -245,18 +246,23 @@ def _current_stream(device) -> int:
 # _WS_KEEP bytes are taken from the caching allocator per call instead.
 _WS: dict = {}
 _WS_KEEP = 64 << 20
+_WS_LOCK = threading.Lock()
 
 
-def workspace(idx: int, stream: int, nbytes: int) -> int:
-    """Device address of at least ``nbytes`` of scratch for work queued on ``stream``; the
-    memory stays owned here (kept) or by a tensor the caller must hold until the launch is
-    queued (returned as the second element)."""
+def workspace(idx: int, stream: int, nbytes: int) -> torch.Tensor:
+    """A device tensor of at least ``nbytes`` of scratch for work queued on ``stream``.
+
+    The caller holds the returned tensor until its launch is queued.  Another host thread
+    that needs more scratch on the same stream replaces the kept tensor (the C call runs
+    without the GIL); the caller's reference keeps the old block out of the caching
+    allocator until its kernels are queued, after which stream order protects it."""
     key = (idx, stream)
-    ws = _WS.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _WS[key] = ws
-    return ws.data_ptr()
+    with _WS_LOCK:
+        ws = _WS.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
+            _WS[key] = ws
+    return ws
 
 
 # 64-bit word indices of the pointer fields in MbGemmDesc (checked at import below)
@@ -272,18 +278,18 @@ def launch(desc: MbGemmDesc, nbytes: int, device) -> None:
     torch.device or an index) with ``nbytes`` of workspace."""
     idx = _device_index(device)
     stream = torch._C._cuda_getCurrentRawStream(idx)
-    ws = None
+    ws = None   # held until mb_gemm has queued the kernels that use it
     if nbytes > 0:
         if nbytes <= _WS_KEEP:
-            desc.workspace = workspace(idx, stream, nbytes)
+            ws = workspace(idx, stream, nbytes)
         else:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
-            desc.workspace = ws.data_ptr()
+        desc.workspace = ws.data_ptr()
         desc.workspace_bytes = nbytes
     status = (_LIB or load()).mb_gemm(ctypes.byref(desc), stream)
     if status:
         check(status)
-    # a per-call ws returns to torch's caching allocator; reuse is ordered on the same stream
+    # ws returns to torch's caching allocator (or stays kept); reuse is ordered on the stream
     del ws
 
 

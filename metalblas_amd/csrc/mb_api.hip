@@ -127,6 +127,10 @@ int ilog2_floor(int64_t v) {
 // fall-back to the plan without scratch.
 constexpr int32_t kFlagStaticScratch = 1 << 30;
 
+// A caller's descriptor carrying an internal flag: the public entry points refuse it (only
+// mb_gemm_noalloc sets kFlagStaticScratch, on its own copy of the descriptor).
+bool internal_flags(const mb_gemm_desc *d) { return d && (d->flags & kFlagStaticScratch); }
+
 int normalise(const mb_gemm_desc *d, Prob &p) {
     if (!d) return MB_ERR_INVALID_ARG;
     if (d->dtype < 0 || d->dtype >= MB_DTYPE_COUNT) return MB_ERR_UNSUPPORTED_DTYPE;
@@ -1183,7 +1187,7 @@ bool plan_packed_peel(const mb_gemm_desc *d, CallPlan &cp, bool sizing) {
         return false;
     if (d->dtype != MB_DTYPE_BF16 && d->dtype != MB_DTYPE_F16) return false;
     if (d->M < 2048 || d->N < 2048 || d->K < 2048 || d->a.col_stride != 1 || d->b.col_stride != 1) return false;
-    if (d->conj_a || d->conj_b || (d->flags & kFlagStaticScratch)) return false;
+    if (d->conj_a || d->conj_b) return false;
     if (!sizing && !d->workspace) return false;
     const int64_t rm = d->M % 256, rn = d->N % 256;
     const bool pm = rm >= 1 && rm <= 16, pn = rn >= 1 && rn <= 16;
@@ -1436,7 +1440,7 @@ extern "C" {
 
 int mb_gemm(const mb_gemm_desc *desc, void *stream) {
     if (!desc) return MB_ERR_INVALID_ARG;
-    if (desc->flags & kFlagStaticScratch) return MB_ERR_INVALID_ARG;
+    if (internal_flags(desc)) return MB_ERR_INVALID_ARG;
     return gemm_impl(desc, stream);
 }
 
@@ -1507,6 +1511,7 @@ int gemm_impl(const mb_gemm_desc *desc, void *stream) {
 extern "C" {
 
 int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
+    if (internal_flags(desc)) return MB_ERR_INVALID_ARG;
     Peel pe;
     if (desc && plan_peel(desc, pe)) {   // the parts run one after another: the largest need
         int64_t ws = 0;
@@ -1527,7 +1532,7 @@ int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc) {
 }
 
 int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
-    if (!info) return MB_ERR_INVALID_ARG;
+    if (!info || internal_flags(desc)) return MB_ERR_INVALID_ARG;
     Plan pl;
     Peel pe;
     CallPlan cp;
@@ -1584,6 +1589,7 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
 }
 
 int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
+    if (internal_flags(desc)) return MB_ERR_INVALID_ARG;
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;

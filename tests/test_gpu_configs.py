@@ -27,7 +27,7 @@ NAMES = [n for g in bench.WORKLOADS for n in bench.WORKLOADS[g]]
 GROUP_OF = {n: g for g in bench.WORKLOADS for n in bench.WORKLOADS[g]}
 
 # oracle rows per workload: more where a row is cheap, fewer on the 8192-wide headline
-ROWS = {"bf16_gemm_8192": 8, "gemv_x@W": 1, "gemv_X8@W": 3, "c64_gemm_2048_conjA": 24,
+ROWS = {"bf16_gemm_8192": 8, "gemv_x@W": 1, "gemv_Wt@x": 48, "gemv_X8@W": 3, "c64_gemm_2048_conjA": 24,
         "i8_gemm_4096": 24}
 
 

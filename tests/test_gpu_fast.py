@@ -121,3 +121,42 @@ def test_split_k_workspace_is_per_stream(dev):
     refs = {1: ref1, 2: ref2, 3: ref3}
     for which, o in outs:
         assert torch.equal(o, refs[which]), f"stream result {which} differs from the serial one"
+
+
+def test_two_threads_share_one_stream_while_the_workspace_grows(dev):
+    """Two host threads queue split-K products of growing size on the same (default) stream
+    through the Python path (addmm: an epilogue never takes the compiled fast path).  Each larger
+    product replaces the kept split-K workspace while the other thread may sit between picking
+    up the old one and queuing its kernels (the C call runs without the GIL); every result must
+    still equal, bit for bit, the same call made from one thread."""
+    import threading
+    from metalblas_amd import _lib
+    g = gen(11)
+    shapes = [(64, 64, 32768), (128, 128, 32768), (192, 192, 32768), (256, 256, 16384)]
+    ops = []
+    for m, n, k in shapes:
+        a, b = rand((m, k), torch.float16, g).to(dev), rand((k, n), torch.float16, g).to(dev)
+        bias = rand((n,), torch.float16, g).to(dev)
+        ops.append((bias, a, b))
+    want = [mb.addmm(*o, beta=0.5, alpha=2.0) for o in ops]
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(order):
+        try:
+            for rnd in range(6):
+                _lib._WS.clear()          # the kept workspace starts small and grows again
+                for i in order:
+                    got = mb.addmm(*ops[i], beta=0.5, alpha=2.0)
+                    if not torch.equal(got, want[i]):
+                        errors.append((rnd, shapes[i]))
+        except Exception as e:   # pragma: no cover - reported below
+            errors.append(repr(e))
+
+    threads = [threading.Thread(target=worker, args=(o,)) for o in ([0, 1, 2, 3], [3, 2, 1, 0])]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors

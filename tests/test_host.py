@@ -136,6 +136,17 @@ def test_abi_rejects_bad_descriptors_before_launch():
     e = torch.empty(0, 8)
     d = _desc(torch.float32, e, a, c=torch.empty(0, 8))
     assert lib.mb_gemm(ctypes.byref(d), None) == 0
+    # the library's internal flag bit (static scratch of mb_gemm_noalloc) is refused by every
+    # entry point that takes a descriptor
+    d = _desc(torch.float32, a, a)
+    d.flags = 1 << 30
+    info = _lib.MbPlanInfo()
+    tiles = (ctypes.c_int32 * 64)()
+    assert lib.mb_gemm(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    assert lib.mb_gemm_noalloc(ctypes.byref(d), None) == _lib.ERR_INVALID_ARG
+    assert lib.mb_plan(ctypes.byref(d), ctypes.byref(info)) == _lib.ERR_INVALID_ARG
+    assert lib.mb_gemm_workspace_bytes(ctypes.byref(d)) == _lib.ERR_INVALID_ARG
+    assert lib.mb_tile_candidates(ctypes.byref(d), tiles, 8) == _lib.ERR_INVALID_ARG
 
 
 # ---- planner decisions at the BASELINE configurations (256 CUs assumed without a GPU) ---------

@@ -83,8 +83,20 @@ def _thin(dev, g, big):
     return W, X, {}
 
 
+def _packed_peel(dev, g, big):
+    # odd leading dimensions copy both operands; with N = 4097 the product is peeled after the
+    # copies (the core on whole 256 x 256 tiles, the last column on the dot GEMV), and copies
+    # plus parts fit the static buffer (34.6 MB), so noalloc runs the same peeled plan.  The
+    # second call (2049^3, 17 MB of copies) is unpeeled.
+    M, N, K = (4096, 4097, 2049) if big else (2049, 2049, 2049)
+    a = rand((M, K), torch.bfloat16, g).to(dev)
+    b = rand((K, N), torch.bfloat16, g).to(dev)
+    return a, b, {}
+
+
 CASES = {"split_k": _split_k, "split_k_addmm": _split_k_addmm, "gemv_x@W": _gemv_xw,
-         "operand_copy": _col_sliced, "complex64_conj": _complex, "thin_W@X8": _thin}
+         "operand_copy": _col_sliced, "complex64_conj": _complex, "thin_W@X8": _thin,
+         "packed_peel": _packed_peel}
 
 
 @pytest.mark.parametrize("case", list(CASES))
