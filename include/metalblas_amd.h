@@ -12,7 +12,10 @@
  *   - The library never allocates device memory and never synchronises.  Kernels are queued
  *     on the caller's stream (a hipStream_t passed as void*; NULL = the null stream).
  *   - Scratch space (split-K partial planes) is provided by the caller: query the size with
- *     mb_gemm_workspace_bytes() for the same descriptor and pass it in desc->workspace.
+ *     mb_gemm_workspace_bytes() for the same descriptor and pass it in desc->workspace.  One
+ *     workspace may serve successive calls on one stream, but a call queues up to several
+ *     kernels (a split-K product and its reduction), so calls queued concurrently from several
+ *     host threads need distinct workspaces, or a lock held across each mb_gemm() call.
  *   - Return value 0 = success, negative = mb_status (see mb_strerror()).
  *   - Thread-safe.  Mutable global state, each guarded by a mutex: the per-process
  *     device-property cache, the plan cache of mb_gemm() (up to 1024 call signatures), and the

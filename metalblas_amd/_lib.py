@@ -11,6 +11,7 @@ There is no CPU fallback: if the library is missing the call raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -242,27 +243,34 @@ def _current_stream(device) -> int:
 
 
 # Split-K workspace kept per (device, stream): the kernels of one stream run in order, so a
-# call's scratch is free again for the next call queued on the same stream.  Workspaces above
-# _WS_KEEP bytes are taken from the caching allocator per call instead.
+# call's scratch is free again for the next call queued on the same stream -- provided the
+# calls' launch sequences do not interleave.  A call queues up to several kernels (a split-K
+# product and its reduction) without the GIL, so two host threads on one stream could queue
+# k1(A), k1(B), reduce(A), reduce(B) and A's reduction would read B's planes.  Each kept
+# workspace therefore has a lock that its user holds while its kernels are queued.
+# Workspaces above _WS_KEEP bytes are taken from the caching allocator per call instead.
 _WS: dict = {}
 _WS_KEEP = 64 << 20
 _WS_LOCK = threading.Lock()
 
 
-def workspace(idx: int, stream: int, nbytes: int) -> torch.Tensor:
-    """A device tensor of at least ``nbytes`` of scratch for work queued on ``stream``.
+def workspace(idx: int, stream: int, nbytes: int):
+    """(tensor, lock): a device tensor of at least ``nbytes`` of scratch for work queued on
+    ``stream``, and the lock to hold while queuing the kernels that use it.
 
-    The caller holds the returned tensor until its launch is queued.  Another host thread
-    that needs more scratch on the same stream replaces the kept tensor (the C call runs
-    without the GIL); the caller's reference keeps the old block out of the caching
-    allocator until its kernels are queued, after which stream order protects it."""
+    The caller keeps the tensor referenced until its launch is queued: another host thread that
+    needs more scratch on the same stream replaces the kept tensor, and the reference keeps the
+    old block out of the caching allocator until then (stream order protects it after)."""
     key = (idx, stream)
     with _WS_LOCK:
-        ws = _WS.get(key)
-        if ws is None or ws.numel() < nbytes:
-            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
-            _WS[key] = ws
-    return ws
+        ent = _WS.get(key)
+        if ent is None or ent[0].numel() < nbytes:
+            t = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
+            ent = _WS[key] = (t, ent[1] if ent is not None else threading.Lock())
+    return ent
+
+
+_NO_LOCK = contextlib.nullcontext()
 
 
 # 64-bit word indices of the pointer fields in MbGemmDesc (checked at import below)
@@ -278,15 +286,16 @@ def launch(desc: MbGemmDesc, nbytes: int, device) -> None:
     torch.device or an index) with ``nbytes`` of workspace."""
     idx = _device_index(device)
     stream = torch._C._cuda_getCurrentRawStream(idx)
-    ws = None   # held until mb_gemm has queued the kernels that use it
+    ws, lock = None, _NO_LOCK   # ws is held until mb_gemm has queued the kernels that use it
     if nbytes > 0:
         if nbytes <= _WS_KEEP:
-            ws = workspace(idx, stream, nbytes)
+            ws, lock = workspace(idx, stream, nbytes)
         else:
             ws = torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx))
         desc.workspace = ws.data_ptr()
         desc.workspace_bytes = nbytes
-    status = (_LIB or load()).mb_gemm(ctypes.byref(desc), stream)
+    with lock:
+        status = (_LIB or load()).mb_gemm(ctypes.byref(desc), stream)
     if status:
         check(status)
     # ws returns to torch's caching allocator (or stays kept); reuse is ordered on the stream

@@ -170,15 +170,16 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
             _lib.launch(desc, ws_bytes, idx)
         return out
     stream = torch._C._cuda_getCurrentRawStream(idx)
-    ws = None   # held until mb_gemm has queued the kernels that use it
+    ws, lock = None, _lib._NO_LOCK   # ws is held until mb_gemm has queued the kernels using it
     if ws_bytes > 0:
         if ws_bytes <= _lib._WS_KEEP:
-            ws = _lib.workspace(idx, stream, ws_bytes)
+            ws, lock = _lib.workspace(idx, stream, ws_bytes)
         else:
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out.device)
         w[_lib.W_WS] = ws.data_ptr()
         w[_lib.W_WS_BYTES] = ws_bytes
-    status = (_lib._LIB or _lib.load()).mb_gemm(ref, stream)
+    with lock:
+        status = (_lib._LIB or _lib.load()).mb_gemm(ref, stream)
     if status:
         _lib.check(status)
     del ws
