@@ -940,6 +940,10 @@ int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
         return MB_OK;
     }
     const bool thin = p.M <= 16 || p.N <= 16;
+    // an explicit tile-family request (the autotuner's candidate, or matmul(tile=...)) on a
+    // product that is not a single vector runs on the matrix cores instead of the GEMV kernels
+    const bool tile_req = p.tile[0] > 0 && p.tile[1] > 0 && !thin_tile(MfmaTile{p.tile[0], p.tile[1], 0, 0, 0}) &&
+                          p.M > 1 && p.N > 1;
     if (p.backend == MB_BACKEND_AUTO && (p.M <= 32 || p.N <= 32) && allow_ws) {
         Plan tp = pl;
         if (plan_thin_mfma(p, tp)) {
@@ -947,7 +951,7 @@ int make_plan(const mb_gemm_desc *d, Plan &pl, bool allow_ws = true) {
             return MB_OK;
         }
     }
-    if (p.backend == MB_BACKEND_GEMV || (p.backend == MB_BACKEND_AUTO && thin)) {
+    if (p.backend == MB_BACKEND_GEMV || (p.backend == MB_BACKEND_AUTO && thin && !tile_req)) {
         if (plan_gemv(p, pl)) {
             if (!allow_ws) drop_splits(pl);
             return MB_OK;
@@ -1593,35 +1597,101 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
     Plan pl;
     int st = make_plan(desc, pl);
     if (st != MB_OK) return st;
-    if (pl.family != MB_FAMILY_MFMA) return 0;
-    MfmaTile list[32];
-    const int n = mfma_list_tiles(pl.p.dt, list, 32);
+    const bool mfma = pl.family == MB_FAMILY_MFMA;
+    const bool gemv = pl.family == MB_FAMILY_GEMV_DOT || pl.family == MB_FAMILY_GEMV_AXPY;
+    if (!mfma && !gemv) return 0;
+    const int dt = desc->dtype;
+    const int bk = 8 * (16 / dtype_size(dt));
     int out = 0;
-    auto emit = [&](const MfmaTile &t) {
+    // plan identities already listed (family, tile, K slices): a request that plans like an
+    // earlier entry is not listed again
+    struct Ident {
+        int family, bm, bn, wm, wn, sched, splits;
+    };
+    Ident seen[48];
+    int nseen = 0;
+    auto ident = [](const Plan &q) {
+        const bool m = q.family == MB_FAMILY_MFMA;
+        return Ident{q.family, m ? q.tile.bm : 0, m ? q.tile.bn : 0, m ? q.tile.wm : 0, m ? q.tile.wn : 0,
+                     m ? q.tile.sched : 0, m ? q.gg.splits : q.gv.splits};
+    };
+    auto fresh = [&](const Ident &x) {
+        for (int i = 0; i < nseen; ++i)
+            if (!memcmp(&seen[i], &x, sizeof(Ident))) return false;
+        if (nseen < 48) seen[nseen++] = x;
+        return true;
+    };
+    auto put = [&](const MfmaTile &t, int split) {
         if (out < cap && tiles) {
             int32_t *q = tiles + 8 * out;
             memset(q, 0, 8 * sizeof(int32_t));
-            q[0] = t.bm; q[1] = t.bn; q[2] = 8 * (16 / dtype_size(pl.p.dt)); q[3] = t.wm; q[4] = t.wn;
-            q[5] = t.sched + 1;
+            if (t.bm > 0) {
+                q[0] = t.bm; q[1] = t.bn; q[2] = bk; q[3] = t.wm; q[4] = t.wn; q[5] = t.sched + 1;
+            }
+            q[6] = split;
         }
         ++out;
     };
-    emit(pl.tile);
-    // thin and deep-K products have one matrix-core tile; a peeled product keeps its peeled plan
-    // (a tile request turns the peeling off)
-    if (thin_tile(pl.tile) || pl.tile.sched == 2) return 1;
+    // entry 0: the static plan (its matrix-core tile, or zeros for a GEMV plan); a tuner runs it
+    // without a request (a tile request turns edge peeling off)
     {
+        // an edge-peeled product runs the peel: entry 0 shows its core (as mb_plan does), and
+        // every whole-product tile is a rival
         Peel pe;
         CallPlan cp;
-        if (plan_peel(desc, pe) || plan_packed_peel(desc, cp, true)) return 1;
+        Plan core;
+        if (plan_peel(desc, pe) && make_plan(&pe.part[0], core) == MB_OK) {
+            put(core.tile, 0);
+        } else if (plan_packed_peel(desc, cp, true)) {
+            put(cp.part[0].tile, 0);
+        } else {
+            put(mfma ? pl.tile : MfmaTile{0, 0, 0, 0, 0}, 0);
+            fresh(ident(pl));
+        }
     }
-    for (int i = 0; i < n && i < 32; ++i) {
-        const MfmaTile &t = list[i];
-        if (t.bm == pl.tile.bm && t.bn == pl.tile.bn && t.wm == pl.tile.wm && t.wn == pl.tile.wn &&
-            t.sched == pl.tile.sched)
-            continue;
-        if (t.bm > 2 * pl.p.M + 32 || t.bn > 2 * pl.p.N + 32 || thin_tile(t) || t.sched == 2) continue;
-        emit(t);
+    // a request: listed when it plans to the requested tile (and K slices) and differs from
+    // every plan listed before
+    auto offer = [&](const MfmaTile &t, int split) {
+        if (out >= cap && tiles) return;
+        mb_gemm_desc d = *desc;
+        d.tile[0] = t.bm; d.tile[1] = t.bn; d.tile[2] = 0; d.tile[3] = t.wm; d.tile[4] = t.wn; d.tile[5] = t.sched + 1;
+        d.tile[6] = d.tile[7] = 0;
+        d.split_k = split;
+        Plan q;
+        if (make_plan(&d, q) != MB_OK || q.family != MB_FAMILY_MFMA) return;
+        if (q.tile.bm != t.bm || q.tile.bn != t.bn || q.tile.sched != t.sched) return;
+        if (split > 0 && q.gg.splits != split) return;
+        if (fresh(ident(q))) put(t, split);
+    };
+    const Prob &p = pl.p;   // the planned problem (a column-major output is the transposed one)
+    if (pl.cplx || !mfma_supported_dtype(dt)) return out;
+    MfmaTile list[32];
+    const int n = mfma_list_tiles(dt, list, 32);
+    const bool f16 = dt == MB_DTYPE_BF16 || dt == MB_DTYPE_F16;
+    // (a) the thin-product kernels, for a bf16 / fp16 product with at most 32 rows or columns
+    //     (the reference times its gemv_bt / flipt / sgpipe kernels against the tiles,
+    //     metalblas/float_dispatch.py:439-481, 516-542)
+    if (f16 && (desc->M <= 32 || desc->N <= 32)) {
+        static const MfmaTile thin[] = {{4, 8, m16::kDotxMaxWaves, 1, 0}, {4, 16, 1, 1, 0}, {64, 16, 4, 1, 0},
+                                        {32, 128, 1, 4, 0}, {32, 256, 1, 4, 0}};
+        for (const MfmaTile &t : thin) offer(t, 0);
+    }
+    // (b) the tile family (matrix-core tiles other than the thin and deep-K schedules), for
+    //     products that are not a single vector
+    if (desc->M > 1 && desc->N > 1) {
+        for (int i = 0; i < n && i < 32; ++i) {
+            const MfmaTile &t = list[i];
+            if (thin_tile(t) || t.sched == 2) continue;
+            if (t.bm > 2 * p.M + 32 || t.bn > 2 * p.N + 32) continue;
+            offer(t, 0);
+        }
+    }
+    // (c) K slices of the static tile: one slice more coarsely or finely split than the
+    //     planner's choice (the reference's split-K candidates, float_dispatch.py:439-481)
+    if (mfma && !thin_tile(pl.tile) && pl.tile.sched != 2 && p.K >= 2048) {
+        const int s = pl.gg.splits;
+        for (int v : {s > 1 ? s / 2 : 0, s > 1 ? 1 : 0, 2 * s})
+            if (v >= 1 && v != s && v <= 64 && p.K / v >= 4 * bk) offer(pl.tile, v);
     }
     return out < cap ? out : cap;
 }

@@ -44,7 +44,7 @@ def device_info() -> dict:
 
 def plan(a, b, *, batch=None, backend=None, tile=None, out_dtype=None, out=None, tuned=False) -> dict:
     """The plan libmetalblas_hip.so would run for ``a @ b`` (2-D or 3-D tensors): kernel
-    family, tile, split-K and workspace.  For tests and reports.  With ``tuned=True`` the tile
+    family, tile, split-K and workspace.  For tests and reports.  With ``tuned=True`` the plan
     the one-shot autotuner already chose for this call signature (``out``'s layout included)
     replaces the static one; nothing is timed here.  ``tile`` is a tile request as matmul's."""
     from . import planner
@@ -61,10 +61,9 @@ def plan(a, b, *, batch=None, backend=None, tile=None, out_dtype=None, out=None,
         c = out if out is not None else torch.empty(M, N, dtype=out_dtype or dtype, device=a.device)
     desc = _lib.make_desc(dtype, Bb, M, N, K, _mat(a), _mat(b), _mat(c), backend=BACKENDS[backend], tile=tile)
     if tuned:
-        tile = planner.cached().get(planner._key(desc, c.device))
-        if tile is not None:
-            for i, v in enumerate(tile):
-                desc.tile[i] = int(v)
+        choice = planner.cached().get(planner._key(desc, c.device))
+        if choice is not None:
+            planner.apply(desc, choice)
     info = _lib.plan(desc)
     return {
         "family": _lib.FAMILY_NAMES.get(info.family, str(info.family)),

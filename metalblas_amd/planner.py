@@ -1,16 +1,20 @@
-"""One-shot, correctness-guarded autotuner over the matrix-core tile family.
+"""One-shot, correctness-guarded autotuner across the kernel families.
 
 Restates the reference's autotuner (metalblas/float_dispatch.py:411-481: ``_probe_params``,
 ``_fastest``, ``_autotune_mppt``) for gfx950:
 
-  * the C planner's static choice (``mb_plan``) is the primary candidate; the other compiled
-    tiles that fit the shape come from ``mb_tile_candidates`` (re-derived for 256 CUs and
-    160 KB of LDS instead of the Apple tables of float_dispatch.py:369-404);
+  * the C planner's static plan is the primary candidate and runs as planned; its rivals come
+    from ``mb_tile_candidates``: the other compiled matrix-core tiles that fit the shape
+    (re-derived for 256 CUs and 160 KB of LDS instead of the Apple tables of
+    float_dispatch.py:369-404), the thin-product kernels for products with at most 32 rows or
+    columns (the reference's gemv_bt / flipt / sgpipe / conv1x1 rivals, float_dispatch.py:
+    439-481, 516-542), and coarser / finer K slices of the static tile (its split-K rivals);
   * each candidate runs once and must agree with the primary within 2% of max|C| (exactly,
     for integer dtypes) before it may be timed (float_dispatch.py:464-468);
   * a rival replaces the primary only if it is faster by ``margin`` (3%, as
     float_dispatch.py:157);
-  * the winner is cached per (device, dtype, batch, M, N, K, layout, alignment) key; with
+  * the winner (None when the static plan stays) is cached per (device, dtype, batch, M, N, K,
+    layout, alignment) key; with
     ``METALBLAS_PLAN_CACHE=<file>`` the cache persists as JSON across processes.
 
 As in the reference (float_dispatch.py:156), tuning is on unless ``METALBLAS_AUTOTUNE=0``,
@@ -129,8 +133,17 @@ def _time(fn, warmup, iters, reps):
     return best
 
 
+def apply(desc, choice) -> None:
+    """Write a tuned choice (8 ints: a tile request and, in entry 6, a K-slice request; 0 = the
+    planner's) into ``desc``."""
+    for i in range(6):
+        desc.tile[i] = int(choice[i])
+    desc.split_k = int(choice[6]) if len(choice) > 6 else 0
+
+
 def tune(desc, a, b, out, bias=None) -> None:
-    """Set ``desc.tile`` to the tuned tile for this problem (no-op when not applicable)."""
+    """Set ``desc``'s tile (and K-slice) request to the tuned choice for this problem (no-op
+    when not applicable or when the static plan won)."""
     if not enabled():
         return
     if desc.batch * desc.M * desc.N * desc.K < _MIN_WORK:
@@ -140,16 +153,15 @@ def tune(desc, a, b, out, bias=None) -> None:
     key = _key(desc, device)
     with _LOCK:
         hit = key in _PLANS
-        tile = _PLANS.get(key)
+        choice = _PLANS.get(key)
     if not hit:
         with torch.cuda.device(device):
-            tile = _autotune(desc, out)
+            choice = _autotune(desc, out)
         with _LOCK:
-            _PLANS[key] = tile
+            _PLANS[key] = choice
             _save_cache()
-    if tile is not None:
-        for i, v in enumerate(tile):
-            desc.tile[i] = int(v)
+    if choice is not None:
+        apply(desc, choice)
 
 
 def _like_out(out):
@@ -165,10 +177,12 @@ def _like_out(out):
 
 
 def _autotune(desc, out):
-    info = _lib.plan(desc)
-    if _lib.FAMILY_NAMES.get(info.family) != "mfma":
-        return None
-    cands = _lib.tile_candidates(desc)
+    """The fastest of the static plan and its rivals (``mb_tile_candidates``: other matrix-core
+    tiles, the thin-product kernels, other K-slice counts), or None when the static plan stays.
+    The static plan runs as planned, without a request (a request would turn edge peeling
+    off); a rival must agree with it (2% of max|C|, exactly for integers) before it is timed
+    and must beat it by MARGIN."""
+    cands = _lib.tile_candidates(desc, 24)
     if len(cands) <= 1:
         return None
     lib = _lib.load()
@@ -176,15 +190,17 @@ def _autotune(desc, out):
     scratch = _like_out(out)
     ref = _like_out(out)
 
-    def runner(tile, dst):
+    def runner(choice, dst):
         d = _lib.MbGemmDesc.from_buffer_copy(desc)
-        for i, v in enumerate(tile):
-            d.tile[i] = int(v)
+        if choice is not None:
+            apply(d, choice)
         if out.dim() == 3:
             d.c = _lib.MbMatrix(ctypes.c_void_p(dst.data_ptr()), dst.stride(1), dst.stride(2), dst.stride(0))
         else:
             d.c = _lib.MbMatrix(ctypes.c_void_p(dst.data_ptr()), dst.stride(0), dst.stride(1), 0)
         nbytes = int(lib.mb_gemm_workspace_bytes(ctypes.byref(d)))
+        if nbytes < 0:
+            _lib.check(nbytes)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=out.device)
         d.workspace = ctypes.c_void_p(ws.data_ptr())
         d.workspace_bytes = nbytes
@@ -193,16 +209,16 @@ def _autotune(desc, out):
             _lib.check(lib.mb_gemm(ctypes.byref(d), ctypes.c_void_p(stream)))
         return fn, ws
 
-    primary_fn, keep0 = runner(cands[0], ref)
+    primary_fn, keep0 = runner(None, ref)
     primary_fn()
     torch.cuda.synchronize()
     is_int = out.dtype in (torch.int8, torch.uint8, torch.int16, torch.int32, torch.int64)
     refv = ref.to(torch.complex64 if ref.is_complex() else torch.float32) if not is_int else ref
     scale = float(refv.abs().max().item()) + 1e-6 if not is_int else 0.0
 
-    runs = [(cands[0], primary_fn, keep0)]
-    for t in cands[1:]:
-        fn, keep = runner(t, scratch)
+    runs = [(None, primary_fn, keep0)]
+    for c in cands[1:]:
+        fn, keep = runner(c, scratch)
         fn()
         torch.cuda.synchronize()
         if is_int:
@@ -212,7 +228,7 @@ def _autotune(desc, out):
             ok = bool(torch.isfinite(sv).all().item()) and \
                 float((sv - refv).abs().max().item()) <= 0.02 * scale
         if ok:
-            runs.append((t, fn, keep))
+            runs.append((tuple(c), fn, keep))
     if len(runs) == 1:
         return None
     bt = out.shape[0] if out.dim() == 3 else 1
@@ -220,5 +236,5 @@ def _autotune(desc, out):
     times = [_time(fn, warmup, iters, reps) for _, fn, _ in runs]
     best = min(range(len(times)), key=times.__getitem__)
     if best and times[best] < times[0] * (1.0 - MARGIN):
-        return tuple(runs[best][0])
-    return tuple(runs[0][0])
+        return runs[best][0]
+    return None

@@ -113,3 +113,54 @@ def test_swizzle_log(dev, swz, dtype):
     a, b = rand((M, K), dtype, g), rand((K, N), dtype, g)
     got = mb.matmul(a.to(dev), b.to(dev), backend="mpp_tensor", swizzle_log=swz)
     assert_parity(got, a, b, tag=f"swizzle_log={swz} {dtype}")
+
+
+# products whose static plan is a thin, GEMV or deep-K kernel, or a tile with K slices: the
+# tuner's rivals span the kernel families (metalblas/float_dispatch.py:439-481, 516-542)
+CROSS = {
+    "thin_n 4096x16x4096": (1, 4096, 16, 4096),
+    "thin_m 256x4096x4096": (1, 256, 4096, 4096),
+    "X8@W 8x16384x4096": (1, 8, 16384, 4096),
+    "W@X8 8192x8x8192": (1, 8192, 8, 8192),
+    "x@W 1x8192x8192": (1, 1, 8192, 8192),
+    "W@x 8192x1x8192": (1, 8192, 1, 8192),
+    "deep-K 128x128x32768": (1, 128, 128, 32768),
+    "bmm 32x1024x128x1024": (32, 1024, 128, 1024),
+}
+
+
+@pytest.mark.parametrize("case", list(CROSS))
+def test_cross_family_candidates_and_tuned_plan_match_oracle(dev, monkeypatch, case):
+    """Every rival the tuner may pick (thin-product kernels, the tile family, other K slices),
+    forced one by one through the C ABI, matches the oracle; then the tuned call does, and a
+    second call of the tuned plan gives the same bits."""
+    from metalblas_amd import _lib
+    monkeypatch.setenv("METALBLAS_AUTOTUNE", "1")
+    monkeypatch.delenv("METALBLAS_PLAN_CACHE", raising=False)
+    planner.clear()
+    dispatch.clear_descriptors()
+    Bb, M, N, K = CROSS[case]
+    g = gen(31)
+    shape_a, shape_b = ((Bb, M, K), (Bb, K, N)) if Bb > 1 else ((M, K), (K, N))
+    a = torch.randn(*shape_a, generator=g).to(torch.bfloat16).to(dev)
+    b = torch.randn(*shape_b, generator=g).to(torch.bfloat16).to(dev)
+    out = torch.empty(*(shape_a[:-1] + (N,)), dtype=torch.bfloat16, device=dev)
+    d = _lib.make_desc(torch.bfloat16, Bb, M, N, K, dispatch._mat(a), dispatch._mat(b), dispatch._mat(out))
+    cands = _lib.tile_candidates(d, 24)
+    assert len(cands) >= 2, cands
+    for c in cands[1:]:
+        out.fill_(float("nan"))
+        dc = _lib.MbGemmDesc.from_buffer_copy(d)
+        planner.apply(dc, c)
+        print(f"{case}: candidate {c}", flush=True)
+        _lib.run(dc, dev)
+        torch.cuda.synchronize()
+        assert_parity_full(out, a, b, rows=6, tag=f"{case} candidate {c}")
+    got = mb.bmm(a, b) if Bb > 1 else mb.matmul(a, b)
+    torch.cuda.synchronize()
+    print(f"{case}: tuned choice {list(planner.cached().values())}", flush=True)
+    assert_parity_full(got, a, b, rows=6, tag=f"{case} tuned")
+    again = mb.bmm(a, b) if Bb > 1 else mb.matmul(a, b)
+    assert torch.equal(again, got)
+    planner.clear()
+    dispatch.clear_descriptors()

@@ -259,8 +259,9 @@ def test_plan_packed_peel():
     # 4097^3 bf16: both operands are copied anyway, so they are copied first (A 4097 x 4160, B
     # 4160 x 4104, B's last column K-contiguous 1 x 4160) and the product is peeled on the
     # copies: the plan reports the 4096^2 core on 256 whole 256 x 256 tiles; the workspace holds
-    # the copies and then the largest part's own need; the tuner gets one candidate (a tile
-    # request would turn the peeling off)
+    # the copies and then the largest part's own need; the tuner's candidates show that core
+    # first (the static plan, run without a request) and whole-product tiles as its rivals (a
+    # tile request turns the peeling off)
     a = torch.empty(4097, 4097, dtype=torch.bfloat16)
     p = _plan(torch.bfloat16, a, a)
     assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile)[:2] == (256, 256)
@@ -269,7 +270,9 @@ def test_plan_packed_peel():
     assert copies <= p.workspace_bytes <= copies + (8 << 20)
     d = _desc(torch.bfloat16, a, a)
     assert _lib.load().mb_gemm_workspace_bytes(ctypes.byref(d)) == p.workspace_bytes
-    assert len(_lib.tile_candidates(d)) == 1
+    cands = _lib.tile_candidates(d, 24)
+    assert cands[0][:2] == (256, 256) and len(cands) > 1
+    assert all(_plan(torch.bfloat16, a, a, tile=c[:6]).workspace_bytes < p.workspace_bytes for c in cands[1:])
     # an explicit tile keeps the whole product (561 tiles of 256 x 128)
     p = _plan(torch.bfloat16, a, a, tile=(256, 128, 64, 2, 4, 2))
     assert tuple(p.tile)[:2] == (256, 128) and tuple(p.grid) == (561, 1, 1)
@@ -325,7 +328,9 @@ def test_plan_deep_k(shape):
     assert p.tile[5] == 3 and tuple(p.tile)[:2] == (64, 64), tuple(p.tile)
     assert 2 <= p.split_k <= 256 // tiles and -(-K // p.split_k) >= 1024 - 63
     assert p.grid[0] == tiles * p.split_k and p.grid[1] == 1
-    assert len(_lib.tile_candidates(_desc(torch.bfloat16, a, b))) == 1
+    # the deep-K plan comes first; the tile family (with its own K slices) is its rival
+    cands = _lib.tile_candidates(_desc(torch.bfloat16, a, b), 24)
+    assert cands[0][5] == 3 and all(c[5] != 3 for c in cands[1:])
     ai, bi = torch.empty(M, K, dtype=torch.int8), torch.empty(K, N, dtype=torch.int8)
     assert _plan(torch.int8, ai, bi).tile[5] != 3
     a2 = torch.empty(M, 4096, dtype=torch.bfloat16)
@@ -389,7 +394,39 @@ def test_tile_candidates_primary_first():
     p = _lib.plan(d)
     cands = _lib.tile_candidates(d)
     assert len(cands) >= 2 and cands[0][:2] == tuple(p.tile[:2])
-    assert len(set(c[:6] for c in cands)) == len(cands)
+    assert len(set(c[:7] for c in cands)) == len(cands)
+
+
+@pytest.mark.parametrize("shape", [(4096, 16, 4096), (256, 4096, 4096), (8, 16384, 16384), (1, 16384, 16384),
+                                   (16384, 1, 16384), (16384, 8, 16384), (2048, 2048, 4096)], ids=str)
+def test_tile_candidates_cross_families(shape):
+    """The tuner's rivals span the kernel families (the reference times gemv_bt / flipt /
+    sgpipe / split-K candidates against its tiles, metalblas/float_dispatch.py:439-481, 516-542):
+    entry 0 is the static plan (zeros for a GEMV plan), every rival plans to exactly the tile and
+    K slices it names, and no two entries plan alike."""
+    M, N, K = shape
+    a, b = torch.empty(M, K, dtype=torch.bfloat16), torch.empty(K, N, dtype=torch.bfloat16)
+    d = _desc(torch.bfloat16, a, b)
+    static = _lib.plan(d)
+    cands = _lib.tile_candidates(d, 24)
+    assert len(cands) >= 2, cands
+    fam = _lib.FAMILY_NAMES[static.family]
+    assert cands[0][:2] == (tuple(static.tile[:2]) if fam == "mfma" else (0, 0))
+    seen = {(static.family, tuple(static.tile[:6]) if fam == "mfma" else (), static.split_k)}
+    thin = {(4, 8), (4, 16), (64, 16), (32, 128), (32, 256)}
+    kinds = set()
+    for c in cands[1:]:
+        p = _plan(torch.bfloat16, a, b, tile=c[:6], split_k=c[6])
+        assert _lib.FAMILY_NAMES[p.family] == "mfma" and tuple(p.tile[:2]) == c[:2], (c, tuple(p.tile))
+        assert c[6] == 0 or p.split_k == c[6]
+        ident = (p.family, tuple(p.tile[:6]), p.split_k)
+        assert ident not in seen, c
+        seen.add(ident)
+        kinds.add("thin" if c[:2] in thin else "split" if c[6] else "tile")
+    if min(M, N) <= 32:
+        assert "thin" in kinds or fam == "mfma" and tuple(static.tile[:2]) in thin
+    if min(M, N) > 1 and max(M, N) > 32:
+        assert "tile" in kinds
 
 
 # ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
