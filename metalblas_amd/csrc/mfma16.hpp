@@ -76,10 +76,6 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t vo
                      : "memory");
 }
 __device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-// Every LDS read of this wave has returned (before an LDS-direct load overwrites what it read).
-__device__ __forceinline__ void lgkm_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-// At most N of this wave's loads are still outstanding.
-template <int N> __device__ __forceinline__ void vm_wait_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 // All but the most recent load have completed (loads retire in issue order).
 __device__ __forceinline__ void vm_wait_but_one() { asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); }
 
@@ -798,6 +794,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 // stage kt + NST - 1 are issued right after the barrier that publishes stage kt, so each
 // workgroup keeps (NST - 1) x 32 KiB of the wide operand on the way.  The matrix cores do
 // 2 MFMAs per 16-deep k-step per wave; they are not the limit.
+template <int N> __device__ __forceinline__ void vm_wait_n() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
 // Output tile and K slice of workgroup `pid` of a 1-D grid of n = tiles x splits workgroups:
 // workgroup i runs on XCD i % 8, and the workgroups of one XCD take consecutive (slice, tile)
@@ -968,7 +965,7 @@ hipError_t launch_deepk16(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hi
 // Ping-pong schedule of the 256 x 256 tile with 8 waves, two per SIMD (waves w and w + 4
 // share SIMD w % 4).  The waves form two groups, 0..3 and 4..7, that alternate between a
 // memory phase (all LDS fragment reads of one stage into registers, plus this wave's
-// share of the LDS-direct prefetch) and a compute phase (the stage's MFMAs back to back,
+// share of the LDS-direct prefetch) and a compute phase (the stage's 32 MFMAs back to back,
 // every operand already in registers).  Group 1 runs one phase behind group 0, so on each
 // SIMD one wave keeps the matrix core busy while the other feeds it; a workgroup barrier
 // separates the phases:
@@ -976,18 +973,12 @@ hipError_t launch_deepk16(bool a_kc, bool b_kc, const GemmArgs &g, dim3 grid, hi
 //   phase      2k                    2k+1                  2k+2
 //   group 0    read stage k,         compute stage k       read stage k+1,
 //              prefetch stage k+1                          prefetch stage k+2
-//   group 1    compute stage k-1     read stage k,         compute stage k
-//                                    prefetch stage k+2
+//   group 1    compute stage k-1,    read stage k          compute stage k,
+//              prefetch stage k+1                          prefetch stage k+2
 //
-// Stage k lives in buffer k % 2 during phases 2k and 2k+1.  Group 0 refills the buffer of
-// stage k-1 (read by both groups by then); group 1 refills the buffer it has just read, once
-// its reads have returned (group 0 read that stage a phase earlier).  Each wave waits for its
-// own loads of a stage at the end of odd phases, before the barrier that publishes it.
-// No wave issues loads while it computes: a wave whose LDS-direct load backs up in the memory
-// pipe stops its MFMA stream.  Measured on MI355X (bf16 8192^3, row-major A and B), moving
-// group 1's loads out of its compute phase took a call from 1.44 M to 1.24 M shader cycles
-// (matrix cores 0.73 -> 0.85 busy); at the board's power limit the clock fell from 1.78 to
-// 1.58 GHz, so the time went from 807 to 783 us (K-contiguous B: 777 -> 729 us).
+// Stage k lives in buffer k % 2 during phases 2k and 2k+1; its buffer is refilled (stage
+// k+2) from phase 2k+2 on, after both groups read it.  Each wave waits for its own prefetch
+// at the end of odd phases, before the barrier that publishes the stage.
 //
 // MS selects the MFMA block: 32 (32 x 32 x 16 / 32 x 32 x 32 int8, 4 k-steps per stage) or 16
 // (16 x 16 x 32 / 16 x 16 x 64 int8, 2 k-steps).  The 16 x 16 form spends less power per flop,
@@ -1083,7 +1074,8 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
             }
         };
-        // loads per prefetch(kt) call: the A segments, the B segments, then the L2-prefetch line
+        // load `op` of prefetch(kt), in the same order: the A segments, the B segments, then the
+        // L2-prefetch line (so the wait for "all but the most recent load" still works)
         constexpr int NOPS = TA::PER_WAVE + TB::PER_WAVE + (PF ? 1 : 0);
         // the wait for this wave's loads of a stage (the L2-prefetch line is left in flight)
         auto vm_wait_stage = [&]() {
@@ -1092,6 +1084,25 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             else
                 vm_wait_all();
         };
+        auto prefetch_op = [&](int kt, int op) {
+            const uint32_t base = smem_lds + (kt & 1) * STAGE;
+            const bool edge = KTAIL && kt >= nfull;
+            const int kleft = klen - kt * BK;
+            if (op < TA::PER_WAVE) {
+                const int seg = wave + op * NW;
+                dma16(ra, base + seg * 1024, edge ? TA::src_offset(seg, lane, lda, rows_a, kleft) : offa[op], kt * stepa);
+            } else if (op < TA::PER_WAVE + TB::PER_WAVE) {
+                const int ib = op - TA::PER_WAVE, seg = wave + ib * NW;
+                dma16(rb, base + TA::BYTES + seg * 1024, edge ? TB::src_offset(seg, lane, ldb, rows_b, kleft) : offb[ib],
+                      kt * stepb);
+            } else if constexpr (PF) {
+                const int kp = kt + kPfDist;
+                const uint32_t po = kp >= nk ? kOOB : (!KTAIL || kp < nfull) ? pfoff
+                                  : pf_assign<BM, BN, A_KC, B_KC, ES>(wave, lane, tm, tn, lda, ldb, rows_a, rows_b, klen - kp * BK);
+                pf_line(pf_on_a ? ra : rb, junk_lds, po, kp * (pf_on_a ? stepa : stepb));
+            }
+        };
+
         typename AccT<T, MS>::type acc[TN][TM];
 #pragma unroll
         for (int i = 0; i < TN; ++i)
@@ -1125,6 +1136,29 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     for (int j = 0; j < TM; ++j) mma_blk<T, MS>(acc[i][j], fb[s][i], fa[s][j]);
             __builtin_amdgcn_s_setprio(0);
         };
+        // the same MFMAs with prefetch(pk)'s loads issued one after each of the first NOPS
+        // MFMAs (every second one for the half-length 16 x 16 MFMAs), so their issue (and the 5
+        // wait states each carries) overlaps the matrix cores instead of delaying the first MFMA
+        constexpr int PF_EVERY = MS == 16 ? 2 : 1;
+        auto compute_stage_pf = [&](bool do_pf, int pk) {
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int s = 0; s < KSTEPS; ++s)
+#pragma unroll
+                for (int i = 0; i < TN; ++i)
+#pragma unroll
+                    for (int j = 0; j < TM; ++j) {
+                        mma_blk<T, MS>(acc[i][j], fb[s][i], fa[s][j]);
+                        const int idx = (s * TN + i) * TM + j;
+                        // a uniform branch; one code path keeps the registers in check
+                        if (idx % PF_EVERY == 0 && idx / PF_EVERY < NOPS) {
+                            __builtin_amdgcn_sched_barrier(0);
+                            if (do_pf) prefetch_op(pk, idx / PF_EVERY);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                    }
+            __builtin_amdgcn_s_setprio(0);
+        };
         auto phase_end = [&]() {
             __builtin_amdgcn_sched_barrier(0);
             __syncthreads();
@@ -1149,19 +1183,10 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                 phase_end();
                 for (int kt = 0; kt < nk; ++kt) {
                     read_stage(kt);                 // phase 2kt+1
-                    if (kt + 2 < nk) {
-                        // stage kt+2 goes into the buffer just read: once this wave's reads
-                        // have returned (group 0 read it in phase 2kt); then wait for stage
-                        // kt+1's loads only (loads retire in issue order)
-                        __builtin_amdgcn_sched_barrier(0);
-                        lgkm_wait_all();
-                        prefetch(kt + 2);
-                        vm_wait_n<NOPS>();
-                    } else {
-                        vm_wait_all();
-                    }
+                    vm_wait_stage();
                     phase_end();
-                    compute_stage();                // phase 2kt+2
+                    compute_stage_pf(kt + 2 < nk, kt + 2);   // phase 2kt+2: prefetch(kt+2) inside
+
                     if (kt + 1 < nk) phase_end();
                 }
             }
