@@ -1084,16 +1084,19 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             else
                 vm_wait_all();
         };
-        auto prefetch_op = [&](int kt, int op) {
+        // load `op` of prefetch(kt), in the same order: the A segments, the B segments, then the
+        // L2-prefetch line.  EDGE: kt is the stage that holds the K edge (its offsets clip at the
+        // slice end; computed here, so the full stages' code carries no select).
+        auto prefetch_op = [&](auto edge_tag, int kt, int op) {
+            constexpr bool EDGE = decltype(edge_tag)::value;
             const uint32_t base = smem_lds + (kt & 1) * STAGE;
-            const bool edge = KTAIL && kt >= nfull;
             const int kleft = klen - kt * BK;
             if (op < TA::PER_WAVE) {
                 const int seg = wave + op * NW;
-                dma16(ra, base + seg * 1024, edge ? TA::src_offset(seg, lane, lda, rows_a, kleft) : offa[op], kt * stepa);
+                dma16(ra, base + seg * 1024, EDGE ? TA::src_offset(seg, lane, lda, rows_a, kleft) : offa[op], kt * stepa);
             } else if (op < TA::PER_WAVE + TB::PER_WAVE) {
                 const int ib = op - TA::PER_WAVE, seg = wave + ib * NW;
-                dma16(rb, base + TA::BYTES + seg * 1024, edge ? TB::src_offset(seg, lane, ldb, rows_b, kleft) : offb[ib],
+                dma16(rb, base + TA::BYTES + seg * 1024, EDGE ? TB::src_offset(seg, lane, ldb, rows_b, kleft) : offb[ib],
                       kt * stepb);
             } else if constexpr (PF) {
                 const int kp = kt + kPfDist;
@@ -1138,9 +1141,13 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
         };
         // the same MFMAs with prefetch(pk)'s loads issued one after each of the first NOPS
         // MFMAs (every second one for the half-length 16 x 16 MFMAs), so their issue (and the 5
-        // wait states each carries) overlaps the matrix cores instead of delaying the first MFMA
+        // wait states each carries) overlaps the matrix cores instead of delaying the first MFMA.
+        // Unconditional: the iterations that prefetch run this body and the last two run
+        // compute_stage.  A per-load condition (VALU compares feeding branches between the
+        // MFMAs) stalled the MFMA stream: MI355X, bf16 8192^3, 1.45 M -> 1.28 M shader cycles
+        // per call once the branches went (K-contiguous B: 1.54 M -> 1.38 M).
         constexpr int PF_EVERY = MS == 16 ? 2 : 1;
-        auto compute_stage_pf = [&](bool do_pf, int pk) {
+        auto compute_stage_pf = [&](auto edge_tag, int pk) {
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int s = 0; s < KSTEPS; ++s)
@@ -1150,10 +1157,9 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
                     for (int j = 0; j < TM; ++j) {
                         mma_blk<T, MS>(acc[i][j], fb[s][i], fa[s][j]);
                         const int idx = (s * TN + i) * TM + j;
-                        // a uniform branch; one code path keeps the registers in check
                         if (idx % PF_EVERY == 0 && idx / PF_EVERY < NOPS) {
                             __builtin_amdgcn_sched_barrier(0);
-                            if (do_pf) prefetch_op(pk, idx / PF_EVERY);
+                            prefetch_op(edge_tag, pk, idx / PF_EVERY);
                             __builtin_amdgcn_sched_barrier(0);
                         }
                     }
@@ -1181,12 +1187,34 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
             } else {
                 if (nk > 1) prefetch(1);            // phase 0
                 phase_end();
-                for (int kt = 0; kt < nk; ++kt) {
+                // iterations kt < pf_end prefetch stage kt+2 (phase 2kt+2); the first pf_full of
+                // them prefetch a stage without a K edge
+                // (uniform values: scalar loop tests, no VALU compare after the MFMAs)
+                const int pf_end = __builtin_amdgcn_readfirstlane(nk - 2 > 0 ? nk - 2 : 0);
+                const int pf_full = __builtin_amdgcn_readfirstlane(
+                    KTAIL ? (nfull - 2 < pf_end ? (nfull - 2 > 0 ? nfull - 2 : 0) : pf_end) : pf_end);
+                int kt = 0;
+                for (; kt < pf_full; ++kt) {
                     read_stage(kt);                 // phase 2kt+1
                     vm_wait_stage();
                     phase_end();
-                    compute_stage_pf(kt + 2 < nk, kt + 2);   // phase 2kt+2: prefetch(kt+2) inside
-
+                    compute_stage_pf(std::false_type{}, kt + 2);   // phase 2kt+2
+                    phase_end();
+                }
+                if constexpr (KTAIL) {
+                    for (; kt < pf_end; ++kt) {     // the stage with the K edge (at most one)
+                        read_stage(kt);
+                        vm_wait_stage();
+                        phase_end();
+                        compute_stage_pf(std::true_type{}, kt + 2);
+                        phase_end();
+                    }
+                }
+                for (; kt < nk; ++kt) {
+                    read_stage(kt);
+                    vm_wait_stage();
+                    phase_end();
+                    compute_stage();
                     if (kt + 1 < nk) phase_end();
                 }
             }
