@@ -44,7 +44,7 @@ PEAK_HBM_GBS = 8000.0
 # FETCH_SIZE x 2 + WRITE_SIZE (KiB x 1024; the factors come from a 1 GiB device copy), from
 # profiles/gemm_bf16_8192_counters.md and profiles/configs_counters.md
 TRAFFIC = {
-    "bf16_gemm_8192": 1.7482e+09,                   # k_gemm16pp<bf16, ...>
+    "bf16_gemm_8192": 1.7862e+09,                   # k_gemm16pp<bf16, ...>
     "gemv_W@x": 5.3750e+08,                         # k_dot_wg
     "gemv_x@W": 5.4540e+08,                         # k_axpy_band (+ its fp32 planes)
     "gemv_X8@W": 5.4015e+08,                        # k_thin16 32 x 128

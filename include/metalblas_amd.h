@@ -184,9 +184,14 @@ int64_t mb_gemm_workspace_bytes(const mb_gemm_desc *desc);
  * metalblas/float_dispatch.py:484-505 (_gemm_plan) and :613-655 (_pick_mpp_tensor_tile). */
 int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info);
 
-/* Autotune candidates: up to `cap` tiles (8 int32 each, the format of desc->tile) worth timing
- * for this descriptor, primary first; returns the count.  Replaces
- * metalblas/float_dispatch.py:369-404 (_mpp_tensor_tile_candidates). */
+/* Autotune candidates: up to `cap` entries of 8 int32 worth timing for this descriptor;
+ * returns the count.  Entry 0 is the static plan (its matrix-core tile, or zeros for a GEMV
+ * plan; a tuner runs it without a request).  Each other entry is a request that plans to a
+ * different kernel: entries 0-5 go to desc->tile, entry 6 to desc->split_k (0 = the planner's
+ * K slices).  The rivals span the kernel families: the other compiled matrix-core tiles, the
+ * thin-product kernels (products with at most 32 rows or columns) and other K-slice counts of
+ * the static tile.  Replaces metalblas/float_dispatch.py:369-404 (_mpp_tensor_tile_candidates)
+ * and the cross-family candidates of :439-481 and :516-542. */
 int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap);
 
 /* Queries.  Replaces metalblas/kernels.py:65-73 (has_metal4) and the chip detection of
