@@ -190,8 +190,14 @@ __device__ __forceinline__ int swz_k16(int row) { return row & 7; }
 // Chunk swizzle of M/N-major rows.  16-bit: {0, 4, 10, 14}[k & 3]; 8-bit: 2 (k & 7), which
 // puts the 8 k-rows x 2 chunks that a 32-lane slice of one ds_read_b64_tr_b8 touches on 16
 // distinct 16-byte bank groups (for 256-byte rows).  Limited to the chunks of one row.
+// 16-bit 128-byte rows (CPR 8): a 32-lane slice of one ds_read_b64_tr_b16 reads 4 chunks of
+// k-rows k0 .. k0 + 3; rows k and k + 1 already sit in opposite halves of the 64 banks, so the
+// swizzle 4 ((k >> 1) & 1) puts k and k + 2 on opposite halves of the row (all 64 banks once);
+// {0, 4, 10, 14} & 7 put them on the same 4 chunks, two LDS cycles per slice instead of one.
 template <int CPR, int ES> __device__ __forceinline__ int swz_mn(int k) {
-    if constexpr (ES == 2) {
+    if constexpr (ES == 2 && CPR == 8) {
+        return 4 * ((k >> 1) & 1);
+    } else if constexpr (ES == 2) {
         const int f = ((k & 1) << 2) | ((k & 2) ? 10 : 0);
         return f & (CPR - 1);
     } else {
@@ -525,7 +531,8 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccT<T,
 // 16-byte store per lane, consecutive lanes on consecutive chunks.  The direct stores of
 // store_tile16 put 16-32 row fragments of 8-16 bytes in every store instruction, which holds
 // products with a short K (where the output dominates the traffic) to about 2.5 TB/s of writes.
-// Taken for plain row-major outputs: no split-K planes, no epilogue, 16-byte aligned rows.
+// Taken for row-major outputs with 16-byte aligned rows and no split-K planes; a fused epilogue
+// is applied in registers before the tile is staged.
 template <class T, int BM, int BN> struct CStage {
     static_assert(sizeof(T) <= 2, "the staged store packs 4 outputs into 8 or 4 bytes");
     static constexpr int PITCH = BN * (int)sizeof(T) + 16;
@@ -533,17 +540,23 @@ template <class T, int BM, int BN> struct CStage {
 };
 
 template <class T> __device__ __forceinline__ bool staged_store_ok(const GemmArgs &g) {
-    return g.splits <= 1 && !g.planes && !g.epilogue && g.c_cs == 1 && ((g.c_rs * (int64_t)sizeof(T)) & 15) == 0 &&
+    return g.splits <= 1 && !g.planes && g.c_cs == 1 && ((g.c_rs * (int64_t)sizeof(T)) & 15) == 0 &&
            (g.batch == 1 || ((g.c_bs * (int64_t)sizeof(T)) & 15) == 0) && (((uintptr_t)g.c) & 15) == 0;
 }
 
 // this wave's accumulators (the block layout of store_tile16) into the staged tile; mw / nw are
-// tile-relative
+// tile-relative and m0 / n0 the tile's origin in C.  A fused epilogue (alpha, beta and the bias
+// read at the output's coordinates) is applied before the one rounding, as store_tile16 does.
 template <class T, int TM, int TN, int MS, int PITCH>
-__device__ __forceinline__ void stage_acc(char *ct, typename AccT<T, MS>::type (&acc)[TN][TM], int mw, int nw,
-                                          int lane) {
+__device__ __forceinline__ void stage_acc(const GemmArgs &g, char *ct, typename AccT<T, MS>::type (&acc)[TN][TM],
+                                          int mw, int nw, int m0, int n0, int bz, int lane) {
     constexpr int NQ = MS * MS / 256;
+    using A = typename Tr<T>::acc;
     const int mrow = lane % MS, nsub = 4 * (lane / MS);
+    // keep the bias addressing from being hoisted above the main loop (its per-row offsets
+    // would be live across the loop in scalar registers and spill)
+    asm volatile("" : "+s"(mw), "+s"(nw), "+s"(m0), "+s"(n0), "+s"(bz));
+    const T *Bb = (const T *)g.bias + bz * g.bias_bs;
 #pragma unroll
     for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -552,8 +565,27 @@ __device__ __forceinline__ void stage_acc(char *ct, typename AccT<T, MS>::type (
             for (int q = 0; q < NQ; ++q) {
                 const int row = mw + j * MS + mrow, col = nw + i * MS + 8 * q + nsub;
                 T o[4];
+                if (!g.epilogue) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
+                    for (int r = 0; r < 4; ++r) o[r] = (T)acc[i][j][4 * q + r];
+                } else {
+                    // bias elements past the edge of C are not read (their outputs are not stored)
+                    const int gm = m0 + row, gn = n0 + col;
+                    T bv[4] = {};
+                    if (g.beta_nz && gm < g.M) {
+                        const T *brow = Bb + gm * g.bias_rs;
+                        if (g.bias_vec && gn + 3 < g.N) {
+                            __builtin_memcpy(bv, brow + gn, 4 * sizeof(T));
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (gn + r < g.N) bv[r] = brow[(int64_t)(gn + r) * g.bias_cs];
+                        }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        o[r] = Tr<T>::down(epi_apply<T>((A)acc[i][j][4 * q + r], bv + r, g.s, g.beta_nz, g.alpha_nz));
+                }
                 char *dst = ct + row * PITCH + col * (int)sizeof(T);
                 if constexpr (sizeof(T) == 2) {
                     uint2 u;
@@ -774,7 +806,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 
         if (staged_store_ok<T>(g)) {
             __syncthreads();   // every wave is done with the operand stages
-            stage_acc<T, TM, TN, 32, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
+            stage_acc<T, TM, TN, 32, CS::PITCH>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
             __syncthreads();
             if (g.c_stream)
                 store_staged<T, BM, BN, 64 * NW, true>(g, smem, m0, n0, bz, tid);
@@ -1221,7 +1253,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
         }
         if (staged_store_ok<T>(g)) {
             __syncthreads();   // both wave groups are done with the operand stages
-            stage_acc<T, TM, TN, MS, CS::PITCH>(smem, acc, wm * WTM, wn * WTN, lane);
+            stage_acc<T, TM, TN, MS, CS::PITCH>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
             __syncthreads();
             if (g.c_stream)
                 store_staged<T, BM, BN, 512, true>(g, smem, m0, n0, bz, tid);
