@@ -45,25 +45,26 @@ PEAK_HBM_GBS = 8000.0
 # profiles/gemm_bf16_8192_counters.md and profiles/configs_counters.md
 TRAFFIC = {
     "bf16_gemm_8192": 1.7862e+09,                   # k_gemm16pp<bf16, ...>
-    "gemv_W@x": 5.3750e+08,                         # k_dot_wg
-    "gemv_x@W": 5.4540e+08,                         # k_axpy_band (+ its fp32 planes)
-    "gemv_X8@W": 5.4015e+08,                        # k_thin16 32 x 128
-    "gemv_W@X8": 5.3940e+08,                        # k_dotx
-    "bf16_2048x4096x2048_rm_rm": 1.0920e+08,        # k_gemm16 128 x 128
-    "bf16_2048x4096x2048_rm_cm": 1.0920e+08,
-    "bf16_2048x4096x2048_cm_rm": 1.0920e+08,
-    "bf16_2048x4096x2048_cm_cm": 1.0920e+08,
-    "bf16_2048x4096x2048_row_sliced": 1.0920e+08,
-    "bf16_2048x4096x2048_col_sliced": 1.0920e+08,
-    "bf16_2048x4096x2048_offset17": 1.0920e+08,
-    "bf16_2048x4096x2048_addmm": 1.0940e+08,
-    "f16_bmm_8x512x512x256": 1.6910e+07,            # k_gemm16 (the tuned tile)
-    "f16_bmm_broadcastB": 8.5260e+06,
-    "f16_splitk_128x128x65536": 3.7850e+07,         # the deep-K k_thin16 64 x 64
-    "c64_gemm_2048_conjA": 3.7540e+08,              # k_gemm_mfma<float> after k_cplx_expand
-    "c64_gemv_8192": 5.3760e+08,                    # k_cdot_wg
-    "i8_gemm_4096": 1.1758e+08,                     # k_gemm16pp<int8, ...>
-    "i32_gemm_256": 3.0060e+06,                     # k_gemm_generic<int32, 16>
+    "gemv_W@x": 5.3746e+08,                         # k_dot_wg
+    "gemv_x@W": 5.4544e+08,                         # k_axpy_band (+ its fp32 planes)
+    "gemv_Wt@x": 5.4544e+08,                        # k_axpy_band, as x@W
+    "gemv_X8@W": 5.4012e+08,                        # k_thin16 32 x 128
+    "gemv_W@X8": 5.3933e+08,                        # k_dotx
+    "bf16_2048x4096x2048_rm_rm": 1.0938e+08,        # k_gemm16 128 x 128
+    "bf16_2048x4096x2048_rm_cm": 1.0938e+08,
+    "bf16_2048x4096x2048_cm_rm": 1.0939e+08,
+    "bf16_2048x4096x2048_cm_cm": 1.0938e+08,
+    "bf16_2048x4096x2048_row_sliced": 1.0938e+08,
+    "bf16_2048x4096x2048_col_sliced": 1.0938e+08,
+    "bf16_2048x4096x2048_offset17": 1.0938e+08,
+    "bf16_2048x4096x2048_addmm": 1.0941e+08,
+    "f16_bmm_8x512x512x256": 2.3209e+07,            # k_gemm16 (the tile the tuner took: 64 x 64)
+    "f16_bmm_broadcastB": 9.6553e+06,               # k_gemm16 128 x 64
+    "f16_splitk_128x128x65536": 3.7852e+07,         # the deep-K k_thin16 64 x 64
+    "c64_gemm_2048_conjA": 3.7532e+08,              # k_gemm_mfma<float> after k_cplx_expand
+    "c64_gemv_8192": 5.3758e+08,                    # k_cdot_wg
+    "i8_gemm_4096": 1.1794e+08,                     # k_gemm16pp<int8, ...>
+    "i32_gemm_256": 3.0065e+06,                     # k_gemm_generic<int32, 16>
 }
 
 

@@ -61,9 +61,9 @@ def probe_params(M, N, K):
     """(warmup, iters, reps) scaled down as kernels get longer (float_dispatch.py:411-418)."""
     work = M * N * K
     if work <= 2_000_000_000:
-        return 5, 20, 3
+        return 5, 20, 5
     if work <= 50_000_000_000:
-        return 2, 5, 3
+        return 3, 10, 5
     return 1, 3, 2
 
 
@@ -118,19 +118,27 @@ def cached() -> dict:
     return dict(_PLANS)
 
 
-def _time(fn, warmup, iters, reps):
-    for _ in range(warmup):
-        fn()
-    best = float("inf")
-    for _ in range(reps):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record()
-        for _ in range(iters):
+def _fastest(fns, warmup, iters, reps):
+    """Per-call times (ms, best of ``reps``) of ``fns``, as the reference's ``_fastest``
+    (metalblas/float_dispatch.py:419-433): every candidate's warmup first, then the timed
+    repetitions round-robin over the candidates, so a clock that is still ramping up (the
+    first call of a shape often comes to an idle GPU) does not favour the candidates timed
+    last."""
+    for fn in fns:
+        for _ in range(warmup):
             fn()
-        e.record()
-        e.synchronize()
-        best = min(best, s.elapsed_time(e) / iters)
-    return best
+    torch.cuda.synchronize()
+    times = [float("inf")] * len(fns)
+    for _ in range(reps):
+        for i, fn in enumerate(fns):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(iters):
+                fn()
+            e.record()
+            e.synchronize()
+            times[i] = min(times[i], s.elapsed_time(e) / iters)
+    return times
 
 
 def apply(desc, choice) -> None:
@@ -233,7 +241,7 @@ def _autotune(desc, out):
         return None
     bt = out.shape[0] if out.dim() == 3 else 1
     warmup, iters, reps = probe_params(bt * desc.M, desc.N, desc.K)
-    times = [_time(fn, warmup, iters, reps) for _, fn, _ in runs]
+    times = _fastest([fn for _, fn, _ in runs], warmup, iters, reps)
     best = min(range(len(times)), key=times.__getitem__)
     if best and times[best] < times[0] * (1.0 - MARGIN):
         return runs[best][0]
