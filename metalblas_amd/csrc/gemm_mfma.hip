@@ -100,7 +100,7 @@ int mfma_list_tiles(int dt, MfmaTile *out, int cap) {
 hipError_t launch_mfma(int dt, const MfmaTile &t, bool a_kc, bool b_kc, const GemmArgs &g, hipStream_t st,
                        LaunchShape *shape) {
     const int tiles = cdiv(g.M, t.bm) * cdiv(g.N, t.bn);
-    dim3 grid(g.persist > 0 ? g.persist : tiles, g.splits, g.batch < 65535 ? g.batch : 65535);
+    dim3 grid(g.persist > 0 ? g.persist : tiles, g.splits, g.zblocks > 0 ? g.zblocks : g.batch < 65535 ? g.batch : 65535);
     const bool dotx = t.bm == 4 && t.bn == 8;   // k_dotx: one wave per 1024 of K
     if (shape) *shape = {grid, dim3(t.bm == 4 && t.bn == 16 ? 256 : dotx ? 64 * m16::dotx_waves(g.K) : 64 * t.wm * t.wn)};
     if (is16(dt) && !(t.bm == 32 && t.bn == 32)) {

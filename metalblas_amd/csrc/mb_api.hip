@@ -598,6 +598,16 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc, bool thin_ok = fal
     // vector stores: C row-major, 4-element groups aligned
     g.vec_ok = p.c.cs == 1 && (p.c.rs % 4) == 0 && aligned(p.c.ptr, 4 * es) &&
                (p.batch == 1 || (p.c.bs % 4) == 0);
+    // Chained one-stage tiles (k_gemm16): a K slice of one stage over many batch entries runs
+    // on fewer z-blocks, each workgroup taking several entries in turn so that the loads of one
+    // entry overlap the epilogue of the one before; about four workgroups per CU remain.  Only
+    // tiles whose staged output fits one operand stage chain.
+    const bool lds_direct = p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8;
+    if (lds_direct && t.sched == 0 && t.bm >= 64 && t.bn >= 64 && g.k_chunk <= BK && p.batch > 1 &&
+        (int64_t)t.bm * (t.bn * es + 16) <= (int64_t)(t.bm + t.bn) * 128) {
+        const int64_t per = std::min<int64_t>(tiles * splits / (4LL * cus), 16);
+        if (per >= 2) g.zblocks = (int)((p.batch + per - 1) / per);
+    }
     pl.family = MB_FAMILY_MFMA;
     pl.tile = t;
     pl.a_kc = a_kc;
@@ -1575,7 +1585,7 @@ int mb_plan(const mb_gemm_desc *desc, mb_plan_info *info) {
             info->grid[0] *= pl.gg.splits;
             info->grid[1] = 1;
         }
-        info->grid[2] = (int)(pl.p.batch < 65535 ? pl.p.batch : 65535);
+        info->grid[2] = pl.gg.zblocks > 0 ? pl.gg.zblocks : (int)(pl.p.batch < 65535 ? pl.p.batch : 65535);
     } else if (pl.family == MB_FAMILY_GENERIC) {
         info->tile[0] = pl.gen_bt;
         info->tile[1] = pl.gen_bt;

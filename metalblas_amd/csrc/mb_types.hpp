@@ -210,6 +210,8 @@ struct GemmArgs {
     int32_t bias_vec;    // bias rows read as 4-element vectors (contiguous, 4-element aligned)
     int32_t persist;     // workgroups of a persistent grid that loops over tiles (0: one per tile)
     int32_t c_stream;    // output larger than the last-level cache: non-temporal output stores
+    int32_t zblocks;     // grid z-blocks when fewer than the batch entries, each workgroup taking
+                         // every zblocks-th entry in turn (0: one per entry, at most 65535)
     EpiScalars s;
 };
 

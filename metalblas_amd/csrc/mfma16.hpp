@@ -704,6 +704,35 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
 
+    // Chained one-stage tiles: when the K slice fits one stage and the grid has fewer z-blocks
+    // than batch entries, each workgroup issues the loads of its next batch entry into the
+    // other buffer before the current entry's epilogue, so the load latency overlaps the
+    // output staging and stores instead of following them (short-K batched products, e.g.
+    // attention scores with a head dimension of 64).  The output is staged in the current
+    // entry's own buffer, which needs the staged tile to fit one stage.
+    const bool chain = CS::BYTES <= STAGE && nk == 1 && (int)gridDim.z < g.batch;
+    int sbuf = 0;          // buffer of the current entry's stage (chain)
+    bool issued = false;   // its loads were issued during the previous entry (chain)
+    // stage 0 of batch entry e into buffer buf (chain)
+    auto load_entry = [&](int e, int buf) {
+        const T *Ae = (const T *)g.a + e * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
+        const T *Be = (const T *)g.b + e * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
+        const i32x4 rae = make_rsrc(Ae), rbe = make_rsrc(Be);
+        const uint32_t base = smem_lds + buf * STAGE;
+#pragma unroll
+        for (int i = 0; i < TA::PER_WAVE; ++i) {
+            const int seg = wave + i * NW;
+            if (TA::SEGS % NW == 0 || seg < TA::SEGS)
+                dma16(rae, base + seg * 1024, KTAIL ? TA::src_offset(seg, lane, lda, rows_a, klen) : offa[i], 0);
+        }
+#pragma unroll
+        for (int i = 0; i < TB::PER_WAVE; ++i) {
+            const int seg = wave + i * NW;
+            if (TB::SEGS % NW == 0 || seg < TB::SEGS)
+                dma16(rbe, base + TA::BYTES + seg * 1024, KTAIL ? TB::src_offset(seg, lane, ldb, rows_b, klen) : offb[i], 0);
+        }
+    };
+
     for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
         // resource bases: element (row0, kbeg) of each operand tile
         const T *Ab = (const T *)g.a + bz * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
@@ -771,6 +800,34 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
                 for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[slot][i], fa[slot][j]);
         };
 
+        if (chain) {
+            if (!issued) load_entry(bz, sbuf);
+            vm_wait_all();   // this wave's loads of the stage (and the previous entry's stores)
+            __syncthreads();
+            char *cur = smem + sbuf * STAGE;
+            read_frags(cur, 0, 0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (s < 3) read_frags(cur, s + 1, (s + 1) & 1);
+                mma_step(s & 1);
+            }
+            issued = bz + (int)gridDim.z < g.batch;
+            __syncthreads();   // every wave is done with this stage; the other buffer is free
+            if (issued) load_entry(bz + gridDim.z, sbuf ^ 1);
+            if (staged_store_ok<T>(g)) {
+                stage_acc<T, TM, TN, 32, CS::PITCH>(g, cur, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
+                __syncthreads();
+                if (g.c_stream)
+                    store_staged<T, BM, BN, 64 * NW, true>(g, cur, m0, n0, bz, tid);
+                else
+                    store_staged<T, BM, BN, 64 * NW, false>(g, cur, m0, n0, bz, tid);
+            } else {
+                store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
+            }
+            __syncthreads();   // the staged tile is read out before its buffer takes a stage
+            sbuf ^= 1;
+            continue;
+        }
         if (nk > 0) {
             load_stage(0, 0);
             vm_wait_but_one();

@@ -807,3 +807,47 @@ def test_dotx(dev, dtype, case):
     assert_parity_full(got, ad, bd, rows=16, tag=tag)
     again = mb.bmm(ad, bd) if case == "bmm" else mb.matmul(ad, bd, **force)
     assert torch.equal(got, again), f"{tag}: repeated call differs"
+
+
+# ---- chained one-stage tiles (short-K batched products) -----------------------------------
+
+@pytest.mark.parametrize("case", [
+    (torch.bfloat16, 96, 512, 512, 64, (64, 128), False, None),
+    (torch.float16, 160, 384, 640, 40, (128, 64), False, None),       # K edge inside the stage
+    (torch.bfloat16, 256, 256, 256, 64, (64, 64), True, None),        # broadcast B (stride 0)
+    (torch.bfloat16, 403, 130, 200, 64, (64, 128), False, None),      # ragged tiles, ragged z
+    (torch.int8, 192, 512, 512, 128, (128, 128), False, None),
+    (torch.uint8, 128, 512, 256, 100, (64, 128), False, None),
+    (torch.bfloat16, 96, 512, 512, 64, (64, 128), False, (0.5, 2.0)),  # fused epilogue, row bias
+    (torch.float16, 160, 384, 640, 40, (128, 64), False, (1.0, 1.0)),
+], ids=str)
+def test_chained_one_stage_tiles(dev, case):
+    """A K slice of one stage over many batch entries runs on fewer z-blocks, each workgroup
+    loading its next entry into the other LDS buffer while it stores the current one.  Checked
+    through the C ABI on every entry (the oracle on the first and last, the oracle-pinned fp64
+    GPU product on all), with a K edge, ragged tile and z ranges, a stride-0 B, 8-bit outputs
+    and a fused epilogue."""
+    from metalblas_amd import _lib
+    dtype, Bb, M, N, K, tile, bcast, epi = case
+    g = gen(Bb + K)
+    a = rand((Bb, M, K), dtype, g).to(dev)
+    b = rand((1 if bcast else Bb, K, N), dtype, g).to(dev)
+    bv = b.expand(Bb, K, N) if bcast else b
+    c = torch.empty(Bb, M, N, dtype=dtype, device=dev)
+    kw = {}
+    bias = None
+    if epi is not None:
+        beta, alpha = epi
+        bias = rand((N,), dtype, g).to(dev)
+        kw = dict(epilogue=(beta, alpha, beta != 0, alpha != 0))
+    d = _lib.make_desc(dtype, Bb, M, N, K, (a, K, 1, M * K), (b, N, 1, 0 if bcast else K * N),
+                       (c, N, 1, M * N), (bias, 0, 1, 0) if bias is not None else None, tile=tile, **kw)
+    p = _lib.plan(d)
+    assert tuple(p.tile[:2]) == tile and p.split_k == 1, tuple(p.tile)
+    assert 0 < p.grid[2] < Bb, f"not chained: grid {tuple(p.grid)}"
+    _lib.run(d, dev)
+    if epi is None:
+        assert_parity_full(c, a, bv, rows=8, tag=f"chained {case}")
+    else:
+        assert_parity_full(c, a, bv, bias=bias.expand(Bb, M, N), beta=epi[0], alpha=epi[1], rows=8,
+                           tag=f"chained {case}")
