@@ -598,12 +598,14 @@ void plan_mfma(const Prob &p, Plan &pl, bool a_kc, bool b_kc, bool thin_ok = fal
     // vector stores: C row-major, 4-element groups aligned
     g.vec_ok = p.c.cs == 1 && (p.c.rs % 4) == 0 && aligned(p.c.ptr, 4 * es) &&
                (p.batch == 1 || (p.c.bs % 4) == 0);
-    // Chained one-stage tiles (k_gemm16): a K slice of one stage over many batch entries runs
-    // on fewer z-blocks, each workgroup taking several entries in turn so that the loads of one
-    // entry overlap the epilogue of the one before; about four workgroups per CU remain.  Only
-    // tiles whose staged output fits one operand stage chain.
-    const bool lds_direct = p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16 || p.dt == MB_DTYPE_I8 || p.dt == MB_DTYPE_U8;
-    if (lds_direct && t.sched == 0 && t.bm >= 64 && t.bn >= 64 && g.k_chunk <= BK && p.batch > 1 &&
+    // Chained batch entries (k_gemm16): a K slice of at most four stages over many batch
+    // entries runs on fewer z-blocks, each workgroup streaming the stages of several entries
+    // through its two LDS buffers so that one entry's first loads overlap the previous entry's
+    // last stage and epilogue; about four workgroups per CU remain.  Only 16-bit tiles of at
+    // most 128 x 128 whose staged output fits one operand stage chain (k_gemm16's CHAIN).
+    const bool f16_family = p.dt == MB_DTYPE_BF16 || p.dt == MB_DTYPE_F16;
+    if (f16_family && t.sched == 0 && t.bm >= 64 && t.bn >= 64 && t.bm * t.bn <= 128 * 128 && g.k_chunk <= 4 * BK &&
+        p.batch > 1 &&
         (int64_t)t.bm * (t.bn * es + 16) <= (int64_t)(t.bm + t.bn) * 128) {
         const int64_t per = std::min<int64_t>(tiles * splits / (4LL * cus), 16);
         if (per >= 2) g.zblocks = (int)((p.batch + per - 1) / per);

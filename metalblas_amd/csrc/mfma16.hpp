@@ -704,34 +704,99 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < (B_KC ? 1 : TN); ++j) fbb[j] = TB::frag_base(wn * WTN, lane, j);
 
-    // Chained one-stage tiles: when the K slice fits one stage and the grid has fewer z-blocks
-    // than batch entries, each workgroup issues the loads of its next batch entry into the
-    // other buffer before the current entry's epilogue, so the load latency overlaps the
-    // output staging and stores instead of following them (short-K batched products, e.g.
-    // attention scores with a head dimension of 64).  The output is staged in the current
-    // entry's own buffer, which needs the staged tile to fit one stage.
-    const bool chain = CS::BYTES <= STAGE && nk == 1 && (int)gridDim.z < g.batch;
-    int sbuf = 0;          // buffer of the current entry's stage (chain)
-    bool issued = false;   // its loads were issued during the previous entry (chain)
-    // stage 0 of batch entry e into buffer buf (chain)
-    auto load_entry = [&](int e, int buf) {
-        const T *Ae = (const T *)g.a + e * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
-        const T *Be = (const T *)g.b + e * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
-        const i32x4 rae = make_rsrc(Ae), rbe = make_rsrc(Be);
-        const uint32_t base = smem_lds + buf * STAGE;
+    // Chained batch entries: a short K slice (at most four stages) over more batch entries than
+    // the grid has z-blocks.  Each workgroup runs the stages of its entries as one stream
+    // through the two LDS buffers: the loads of the stream's next stage, which is the next
+    // entry's first stage after an entry's last, are issued before the current stage's
+    // MFMAs, so the next entry's load latency overlaps this entry's last stage and epilogue
+    // instead of following them (short-K batched products, e.g. attention scores with a
+    // head dimension of 64).  The output is staged in the buffer of the entry's last stage,
+    // which needs the staged tile to fit one stage (compiled for 16-bit tiles of at most
+    // 128 x 128: in the 8-bit tiles the second loop cost a wave per SIMD of occupancy).
+    constexpr bool CHAIN = ES == 2 && CS::BYTES <= STAGE && BM * BN <= 128 * 128;   // tiles that may chain
+    if (CHAIN && nk >= 1 && nk <= 4 && (int)gridDim.z < g.batch) {
+        // stage kt of batch entry e into buffer buf
+        auto load_es = [&](int e, int kt, int buf) {
+            const T *Ae = (const T *)g.a + e * g.a_bs + (A_KC ? (int64_t)m0 * lda + kbeg : (int64_t)kbeg * lda + m0);
+            const T *Be = (const T *)g.b + e * g.b_bs + (B_KC ? (int64_t)n0 * ldb + kbeg : (int64_t)kbeg * ldb + n0);
+            const i32x4 rae = make_rsrc(Ae), rbe = make_rsrc(Be);
+            const uint32_t base = smem_lds + buf * STAGE;
+            const bool full = !KTAIL || kt < nfull;
+            const int kleft = klen - kt * BK;
 #pragma unroll
-        for (int i = 0; i < TA::PER_WAVE; ++i) {
-            const int seg = wave + i * NW;
-            if (TA::SEGS % NW == 0 || seg < TA::SEGS)
-                dma16(rae, base + seg * 1024, KTAIL ? TA::src_offset(seg, lane, lda, rows_a, klen) : offa[i], 0);
-        }
+            for (int i = 0; i < TA::PER_WAVE; ++i) {
+                const int seg = wave + i * NW;
+                if (TA::SEGS % NW == 0 || seg < TA::SEGS)
+                    dma16(rae, base + seg * 1024, full ? offa[i] : TA::src_offset(seg, lane, lda, rows_a, kleft),
+                          kt * stepa);
+            }
 #pragma unroll
-        for (int i = 0; i < TB::PER_WAVE; ++i) {
-            const int seg = wave + i * NW;
-            if (TB::SEGS % NW == 0 || seg < TB::SEGS)
-                dma16(rbe, base + TA::BYTES + seg * 1024, KTAIL ? TB::src_offset(seg, lane, ldb, rows_b, klen) : offb[i], 0);
+            for (int i = 0; i < TB::PER_WAVE; ++i) {
+                const int seg = wave + i * NW;
+                if (TB::SEGS % NW == 0 || seg < TB::SEGS)
+                    dma16(rbe, base + TA::BYTES + seg * 1024, full ? offb[i] : TB::src_offset(seg, lane, ldb, rows_b, kleft),
+                          kt * stepb);
+            }
+        };
+        typename AccV<T>::type acc[TN][TM];
+        auto zero_acc = [&]() {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+        };
+        uint4 fa[2][TM], fb[2][TN];
+        auto read_frags = [&](const char *cur, int s, int slot) {
+#pragma unroll
+            for (int j = 0; j < TM; ++j) fa[slot][j] = TA::frag(cur, fba[A_KC ? 0 : j], lane, s, A_KC ? j : 0);
+#pragma unroll
+            for (int i = 0; i < TN; ++i) fb[slot][i] = TB::frag(cur + TA::BYTES, fbb[B_KC ? 0 : i], lane, s, B_KC ? i : 0);
+        };
+        auto mma_step = [&](int slot) {
+#pragma unroll
+            for (int i = 0; i < TN; ++i)
+#pragma unroll
+                for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[slot][i], fa[slot][j]);
+        };
+        zero_acc();
+        int e = blockIdx.z, kt = 0, buf = 0;
+        load_es(e, 0, 0);
+        while (true) {
+            vm_wait_all();     // this wave's loads of stage (e, kt), and earlier stores
+            __syncthreads();   // stage (e, kt) landed everywhere; the other buffer is read out
+            const bool last = kt + 1 == nk;
+            const int ne = last ? e + (int)gridDim.z : e, nkt = last ? 0 : kt + 1;
+            if (ne < g.batch) load_es(ne, nkt, buf ^ 1);
+            char *cur = smem + buf * STAGE;
+            read_frags(cur, 0, 0);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                if (s < 3) read_frags(cur, s + 1, (s + 1) & 1);
+                mma_step(s & 1);
+            }
+            if (last) {
+                __syncthreads();   // every wave is done with this stage before it holds the output
+                if (staged_store_ok<T>(g)) {
+                    stage_acc<T, TM, TN, 32, CS::PITCH>(g, cur, acc, wm * WTM, wn * WTN, m0, n0, e, lane);
+                    __syncthreads();
+                    if (g.c_stream)
+                        store_staged<T, BM, BN, 64 * NW, true>(g, cur, m0, n0, e, tid);
+                    else
+                        store_staged<T, BM, BN, 64 * NW, false>(g, cur, m0, n0, e, tid);
+                } else {
+                    store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, e, ks, lane);
+                }
+                zero_acc();
+                if (ne >= g.batch) break;
+            }
+            e = ne;
+            kt = nkt;
+            buf ^= 1;
         }
-    };
+        return;
+    }
 
     for (int bz = blockIdx.z; bz < g.batch; bz += gridDim.z) {
         // resource bases: element (row0, kbeg) of each operand tile
@@ -800,34 +865,6 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
                 for (int j = 0; j < TM; ++j) mma16<T>(acc[i][j], fb[slot][i], fa[slot][j]);
         };
 
-        if (chain) {
-            if (!issued) load_entry(bz, sbuf);
-            vm_wait_all();   // this wave's loads of the stage (and the previous entry's stores)
-            __syncthreads();
-            char *cur = smem + sbuf * STAGE;
-            read_frags(cur, 0, 0);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                if (s < 3) read_frags(cur, s + 1, (s + 1) & 1);
-                mma_step(s & 1);
-            }
-            issued = bz + (int)gridDim.z < g.batch;
-            __syncthreads();   // every wave is done with this stage; the other buffer is free
-            if (issued) load_entry(bz + gridDim.z, sbuf ^ 1);
-            if (staged_store_ok<T>(g)) {
-                stage_acc<T, TM, TN, 32, CS::PITCH>(g, cur, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
-                __syncthreads();
-                if (g.c_stream)
-                    store_staged<T, BM, BN, 64 * NW, true>(g, cur, m0, n0, bz, tid);
-                else
-                    store_staged<T, BM, BN, 64 * NW, false>(g, cur, m0, n0, bz, tid);
-            } else {
-                store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
-            }
-            __syncthreads();   // the staged tile is read out before its buffer takes a stage
-            sbuf ^= 1;
-            continue;
-        }
         if (nk > 0) {
             load_stage(0, 0);
             vm_wait_but_one();

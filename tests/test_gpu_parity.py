@@ -809,24 +809,27 @@ def test_dotx(dev, dtype, case):
     assert torch.equal(got, again), f"{tag}: repeated call differs"
 
 
-# ---- chained one-stage tiles (short-K batched products) -----------------------------------
+# ---- chained batch entries (short-K batched products) -----------------------------------
 
 @pytest.mark.parametrize("case", [
     (torch.bfloat16, 96, 512, 512, 64, (64, 128), False, None),
     (torch.float16, 160, 384, 640, 40, (128, 64), False, None),       # K edge inside the stage
     (torch.bfloat16, 256, 256, 256, 64, (64, 64), True, None),        # broadcast B (stride 0)
     (torch.bfloat16, 403, 130, 200, 64, (64, 128), False, None),      # ragged tiles, ragged z
-    (torch.int8, 192, 512, 512, 128, (128, 128), False, None),
-    (torch.uint8, 128, 512, 256, 100, (64, 128), False, None),
     (torch.bfloat16, 96, 512, 512, 64, (64, 128), False, (0.5, 2.0)),  # fused epilogue, row bias
     (torch.float16, 160, 384, 640, 40, (128, 64), False, (1.0, 1.0)),
+    (torch.bfloat16, 64, 1024, 1024, 128, (64, 128), False, None),   # two stages per entry
+    (torch.float16, 96, 512, 384, 200, (128, 64), False, None),       # four stages, K edge
+    (torch.float16, 96, 512, 512, 192, (64, 64), False, (1.0, 0.0)),  # three stages, alpha 0
+    (torch.bfloat16, 100, 512, 512, 256, (64, 64), True, (0.5, 2.0)),
 ], ids=str)
-def test_chained_one_stage_tiles(dev, case):
-    """A K slice of one stage over many batch entries runs on fewer z-blocks, each workgroup
-    loading its next entry into the other LDS buffer while it stores the current one.  Checked
+def test_chained_batch_entries(dev, case):
+    """A short K slice (one to four stages) over many batch entries runs on fewer z-blocks,
+    each workgroup streaming the stages of its entries through two LDS buffers (the next
+    entry's first stage loads during the current entry's last stage and epilogue).  Checked
     through the C ABI on every entry (the oracle on the first and last, the oracle-pinned fp64
-    GPU product on all), with a K edge, ragged tile and z ranges, a stride-0 B, 8-bit outputs
-    and a fused epilogue."""
+    GPU product on all), with a K edge, ragged tile and z ranges, a stride-0 B and a fused
+    epilogue (16-bit tiles: the 8-bit ones do not chain)."""
     from metalblas_amd import _lib
     dtype, Bb, M, N, K, tile, bcast, epi = case
     g = gen(Bb + K)

@@ -634,10 +634,11 @@ def test_counter_report_derives_clock_busy_and_traffic(tmp_path):
     assert r["fetch_bytes"] == 3 * 1024 * 2 and r["write_bytes"] == 2 * 1024 and r["traffic_x_alg"] == 1.0
 
 
-def test_chained_one_stage_plans():
+def test_chained_batch_plans():
     """Short-K batched products on small matrix-core tiles run on fewer z-blocks than batch
-    entries (each workgroup chains several one-stage entries); a second stage, a tile whose
-    staged output does not fit one stage, or too few tiles keep one z-block per entry."""
+    entries (each workgroup streams the stages of several entries); more than four stages, a
+    tile whose staged output does not fit one stage, an 8-bit tile, or too few tiles keep one
+    z-block per entry."""
     def z(B, M, N, K, tile, dtype=torch.bfloat16):
         a = torch.empty(1, dtype=dtype)
         d = _lib.make_desc(dtype, B, M, N, K, (a, K, 1, M * K), (a, N, 1, K * N), (a, N, 1, M * N), tile=tile)
@@ -646,7 +647,8 @@ def test_chained_one_stage_plans():
         return p.grid[2]
     assert z(96, 512, 512, 64, (64, 128)) == 32           # 3072 tiles: 3 entries per workgroup
     assert z(48, 2048, 2048, 64, (128, 64)) == 3          # at most 16 entries per workgroup
-    assert z(96, 512, 512, 128, (64, 128)) == 96          # two stages
+    assert z(96, 512, 512, 128, (64, 128)) == 32          # two stages
+    assert z(96, 512, 512, 320, (64, 128)) == 96          # five stages
     assert z(96, 512, 512, 64, (128, 128)) == 96          # staged 128 x 128 output > one stage
     assert z(8, 512, 512, 64, (64, 128)) == 8             # too few tiles
-    assert z(192, 512, 512, 128, (128, 128), torch.int8) == 64
+    assert z(192, 512, 512, 128, (128, 128), torch.int8) == 192   # 16-bit tiles only
