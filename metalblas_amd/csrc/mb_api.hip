@@ -1699,11 +1699,14 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
         }
     }
     // (c) K slices of the static tile: one slice more coarsely or finely split than the
-    //     planner's choice (the reference's split-K candidates, float_dispatch.py:439-481)
-    if (mfma && !thin_tile(pl.tile) && pl.tile.sched != 2 && p.K >= 2048) {
+    //     planner's choice (the reference's split-K candidates, float_dispatch.py:439-481);
+    //     the deep-K schedule halves or doubles its slice count (unsplit, its few tiles would
+    //     leave almost every CU idle)
+    if (mfma && !thin_tile(pl.tile) && p.K >= 2048) {
         const int s = pl.gg.splits;
-        for (int v : {s > 1 ? s / 2 : 0, s > 1 ? 1 : 0, 2 * s})
-            if (v >= 1 && v != s && v <= 64 && p.K / v >= 4 * bk) offer(pl.tile, v);
+        const bool deep = pl.tile.sched == 2;
+        for (int v : {s > 1 ? s / 2 : 0, s > 1 && !deep ? 1 : 0, 2 * s})
+            if (v >= 1 && v != s && v <= (deep ? 128 : 64) && p.K / v >= 4 * bk) offer(pl.tile, v);
     }
     return out < cap ? out : cap;
 }

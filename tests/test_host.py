@@ -328,9 +328,13 @@ def test_plan_deep_k(shape):
     assert p.tile[5] == 3 and tuple(p.tile)[:2] == (64, 64), tuple(p.tile)
     assert 2 <= p.split_k <= 256 // tiles and -(-K // p.split_k) >= 1024 - 63
     assert p.grid[0] == tiles * p.split_k and p.grid[1] == 1
-    # the deep-K plan comes first; the tile family (with its own K slices) is its rival
+    # the deep-K plan comes first; its rivals are the tile family (with its own K slices) and
+    # the deep-K schedule at half and twice the slice count
     cands = _lib.tile_candidates(_desc(torch.bfloat16, a, b), 24)
-    assert cands[0][5] == 3 and all(c[5] != 3 for c in cands[1:])
+    assert cands[0][5] == 3
+    # (a request is listed only when it plans to exactly that many slices of whole stages)
+    deep = sorted(c[6] for c in cands[1:] if c[5] == 3)
+    assert deep and set(deep) <= {p.split_k // 2, 2 * p.split_k}, (deep, p.split_k)
     ai, bi = torch.empty(M, K, dtype=torch.int8), torch.empty(K, N, dtype=torch.int8)
     assert _plan(torch.int8, ai, bi).tile[5] != 3
     a2 = torch.empty(M, 4096, dtype=torch.bfloat16)
