@@ -236,9 +236,8 @@ __global__ __launch_bounds__(256) void k_pack(PackArgs a) {
 // shares the row's misalignment (8-element chunks are 16 bytes), so the cut is wave-uniform.
 // The second chunk is read only when it starts before the row's end, so every read lies in a
 // page that holds a valid element.  Grid as k_pack, with 8-element chunks.
-__global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
+__device__ __forceinline__ void pack16_rows(const PackArgs &a, int64_t ci) {
     const int64_t chunks = a.cols_p / 8;
-    const int64_t ci = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (ci >= chunks) return;
     const int64_t c0 = ci * 8;
     for (int64_t bz = blockIdx.z; bz < a.batch; bz += gridDim.z) {
@@ -277,6 +276,20 @@ __global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
             *(uint4 *)(dst + r * a.d_rs + c0) = v;
         }
     }
+}
+
+__global__ __launch_bounds__(256) void k_pack16_rows(PackArgs a) {
+    pack16_rows(a, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// Both operands of a product in one launch: blocks [0, nx0) of x copy a0, the rest a1 (rows
+// and batches grid-stride over the shared y and z extents).  One launch instead of two saves
+// the second dispatch and its ramp-up (both operands are copied for misaligned rows).
+__global__ __launch_bounds__(256) void k_pack16_rows2(PackArgs a0, PackArgs a1, int nx0) {
+    if ((int)blockIdx.x < nx0)
+        pack16_rows(a0, (int64_t)blockIdx.x * 256 + threadIdx.x);
+    else
+        pack16_rows(a1, (int64_t)(blockIdx.x - nx0) * 256 + threadIdx.x);
 }
 
 // Bhat expansion (CplxExpandArgs): thread per (n, k pair-block) writes the two K-adjacent
@@ -326,11 +339,28 @@ hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// 16-bit rows contiguous in source and destination, destination rows 16-byte aligned
+static bool pack16_rows_ok(const PackArgs &a) {
+    return a.es == 2 && a.contig_cols && a.s_cs == 1 && a.d_cs == 1 && a.cols_p % 8 == 0 && a.d_rs % 8 == 0 &&
+           ((uintptr_t)a.dst & 15) == 0 && (a.d_bs % 8) == 0;
+}
+
+hipError_t launch_pack2(const PackArgs &a0, const PackArgs &a1, hipStream_t st) {
+    if (!pack16_rows_ok(a0) || !pack16_rows_ok(a1)) {
+        hipError_t e = launch_pack(a0, st);
+        return e != hipSuccess ? e : launch_pack(a1, st);
+    }
+    const int64_t nx0 = (a0.cols_p / 8 + 255) / 256, nx1 = (a1.cols_p / 8 + 255) / 256;
+    const int64_t rows = std::max(a0.rows_p, a1.rows_p), batch = std::max(a0.batch, a1.batch);
+    dim3 grid((unsigned)(nx0 + nx1), (unsigned)(rows < 65535 ? rows : 65535), (unsigned)(batch < 65535 ? batch : 65535));
+    hipLaunchKernelGGL(k_pack16_rows2, grid, dim3(256), 0, st, a0, a1, (int)nx0);
+    return hipGetLastError();
+}
+
 hipError_t launch_pack(const PackArgs &a, hipStream_t st) {
     const int64_t inner_n = a.contig_cols ? a.cols_p : a.rows_p;
     const int64_t outer_n = a.contig_cols ? a.rows_p : a.cols_p;
-    if (a.es == 2 && a.contig_cols && a.s_cs == 1 && a.d_cs == 1 && a.cols_p % 8 == 0 && a.d_rs % 8 == 0 &&
-        ((uintptr_t)a.dst & 15) == 0 && (a.d_bs % 8) == 0) {
+    if (pack16_rows_ok(a)) {
         dim3 grid((unsigned)((a.cols_p / 8 + 255) / 256), (unsigned)(outer_n < 65535 ? outer_n : 65535),
                   (unsigned)(a.batch < 65535 ? a.batch : 65535));
         hipLaunchKernelGGL(k_pack16_rows, grid, dim3(256), 0, st, a);

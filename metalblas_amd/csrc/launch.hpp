@@ -109,6 +109,8 @@ struct CplxExpandArgs {
 // gemm_generic.hip
 hipError_t launch_cplx_expand(const CplxExpandArgs &a, hipStream_t st);
 hipError_t launch_pack(const PackArgs &a, hipStream_t st);
+// two operand copies in one launch when both are 16-bit row copies (else two launches)
+hipError_t launch_pack2(const PackArgs &a0, const PackArgs &a1, hipStream_t st);
 // bt: the square output tile, 64, 32 or 16
 hipError_t launch_generic(int dt, int bt, const GemmArgs &g, hipStream_t st, LaunchShape *shape);
 hipError_t launch_fill(int dt, const GemmArgs &g, hipStream_t st);

@@ -377,7 +377,9 @@ int b_orient(const Prob &p) { return p.b.rs == 1 ? 1 : p.b.cs == 1 ? 0 : -1; }
 
 // Can the matrix-core loaders stream this operand in place?  16-byte aligned base, leading
 // dimension and batch stride, and the contiguous extent a multiple of 16 bytes (chunks never
-// straddle the end of a row).
+// straddle the end of a row).  The LDS-direct loads would take misaligned rows too (their
+// buffer loads accept any byte address), but misaligned they slowed the matrix-core kernels
+// down by more than the operand copies cost, so such operands are copied.
 bool operand_ok(const Operand &o, int orient, bool is_a, const Prob &p) {
     const int es = dtype_size(p.dt), E = 16 / es;
     if (orient < 0) return false;
@@ -1014,15 +1016,15 @@ int run_plan(Plan &pl, const mb_gemm_desc *d, hipStream_t st, LaunchShape *shape
     hipError_t e = hipSuccess;
     if (pl.ws_bytes > 0 && (!d->workspace || d->workspace_bytes < pl.ws_bytes)) return MB_ERR_WORKSPACE;
     char *wsb = (char *)d->workspace;
-    for (int which = 0; which < 2; ++which) {
-        PackOp &pk = pl.pack[which];
-        if (!pk.on) continue;
-        pk.a.dst = wsb + pk.off;
-        e = launch_pack(pk.a, st);
-        if (e != hipSuccess) return MB_ERR_LAUNCH;
-        if (which == 0) pl.gg.a = pk.a.dst;
-        else pl.gg.b = pk.a.dst;
-    }
+    for (int which = 0; which < 2; ++which)
+        if (pl.pack[which].on) pl.pack[which].a.dst = wsb + pl.pack[which].off;
+    if (pl.pack[0].on && pl.pack[1].on)
+        e = launch_pack2(pl.pack[0].a, pl.pack[1].a, st);
+    else if (pl.pack[0].on || pl.pack[1].on)
+        e = launch_pack(pl.pack[pl.pack[0].on ? 0 : 1].a, st);
+    if (e != hipSuccess) return MB_ERR_LAUNCH;
+    if (pl.pack[0].on) pl.gg.a = pl.pack[0].a.dst;
+    if (pl.pack[1].on) pl.gg.b = pl.pack[1].a.dst;
     switch (pl.family) {
         case MB_FAMILY_NONE:
             return MB_OK;
@@ -1498,11 +1500,18 @@ int gemm_impl(const mb_gemm_desc *desc, void *stream) {
         // workspace after the copies
         if (!desc->workspace || desc->workspace_bytes < call_ws_bytes(cp)) return MB_ERR_WORKSPACE;
         char *wsb = (char *)desc->workspace;
+        PackArgs a[3];
         for (int i = 0; i < cp.ncopy; ++i) {
-            PackArgs a = cp.copy[i].a;
-            a.dst = wsb + cp.copy[i].off;
-            if (launch_pack(a, (hipStream_t)stream) != hipSuccess) return MB_ERR_LAUNCH;
+            a[i] = cp.copy[i].a;
+            a[i].dst = wsb + cp.copy[i].off;
         }
+        int i = 0;
+        if (cp.ncopy >= 2) {   // the copies of A and B in one launch
+            if (launch_pack2(a[0], a[1], (hipStream_t)stream) != hipSuccess) return MB_ERR_LAUNCH;
+            i = 2;
+        }
+        for (; i < cp.ncopy; ++i)
+            if (launch_pack(a[i], (hipStream_t)stream) != hipSuccess) return MB_ERR_LAUNCH;
         mb_gemm_desc rest = *desc;
         rest.workspace = wsb + cp.copy_bytes;
         rest.workspace_bytes = desc->workspace_bytes - cp.copy_bytes;
