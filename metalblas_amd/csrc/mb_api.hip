@@ -1698,12 +1698,20 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
         for (const MfmaTile &t : thin) offer(t, 0);
     }
     // (b) the tile family (matrix-core tiles other than the thin and deep-K schedules), for
-    //     products that are not a single vector
+    //     products that are not a single vector.  When the static tile already gives every CU
+    //     two tiles, tiles of less than a quarter of its area are not offered: they load more
+    //     bytes per flop and cannot win there, and timing them (the 32 x 32 register-staged
+    //     tile takes tens of milliseconds at 8192^3) only delays the first call and heats the
+    //     board before the work that follows
     if (desc->M > 1 && desc->N > 1) {
+        const int64_t static_tiles =
+            mfma ? ((p.M + pl.tile.bm - 1) / pl.tile.bm) * ((p.N + pl.tile.bn - 1) / pl.tile.bn) * p.batch : 0;
+        const bool plenty = static_tiles >= 2LL * dev_info().cus;
         for (int i = 0; i < n && i < 32; ++i) {
             const MfmaTile &t = list[i];
             if (thin_tile(t) || t.sched == 2) continue;
             if (t.bm > 2 * p.M + 32 || t.bn > 2 * p.N + 32) continue;
+            if (plenty && 4LL * t.bm * t.bn < (int64_t)pl.tile.bm * pl.tile.bn) continue;
             offer(t, 0);
         }
     }

@@ -433,6 +433,18 @@ def test_tile_candidates_cross_families(shape):
         assert "tile" in kinds
 
 
+def test_tile_candidates_skip_small_tiles_on_large_products():
+    # 8192^3: the static 256 x 256 tile gives every CU four tiles, so tiles of less than a
+    # quarter of its area (128 x 64 and smaller, the register-staged 32 x 32) are not timed;
+    # 2048 x 2048 x 4096 (one 128 x 128 tile per CU) keeps the whole family
+    a = torch.empty(8192, 8192, dtype=torch.bfloat16)
+    cands = _lib.tile_candidates(_desc(torch.bfloat16, a, a), 24)
+    assert all(c[0] * c[1] * 4 >= 256 * 256 for c in cands) and len(cands) >= 5, cands
+    a2, b2 = torch.empty(2048, 4096, dtype=torch.bfloat16), torch.empty(4096, 2048, dtype=torch.bfloat16)
+    cands = _lib.tile_candidates(_desc(torch.bfloat16, a2, b2), 24)
+    assert any(c[:2] == (64, 64) for c in cands) and any(c[:2] == (32, 32) for c in cands), cands
+
+
 # ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
 
 @pytest.mark.parametrize("dt", [torch.int8, torch.uint8, torch.bfloat16, torch.float16, torch.float32], ids=str)
