@@ -1699,14 +1699,16 @@ int mb_tile_candidates(const mb_gemm_desc *desc, int32_t *tiles, int cap) {
     }
     // (b) the tile family (matrix-core tiles other than the thin and deep-K schedules), for
     //     products that are not a single vector.  When the static tile already gives every CU
-    //     two tiles, tiles of less than a quarter of its area are not offered: they load more
-    //     bytes per flop and cannot win there, and timing them (the 32 x 32 register-staged
-    //     tile takes tens of milliseconds at 8192^3) only delays the first call and heats the
-    //     board before the work that follows
+    //     two tiles over a K of at least 1024, tiles of less than a quarter of its area are not
+    //     offered: they load more bytes per flop and cannot win there, and timing them (the
+    //     32 x 32 register-staged tile takes tens of milliseconds at 8192^3) only delays the
+    //     first call and heats the board before the work that follows.  Over a short K the
+    //     small tiles stay (chained batch entries on them beat the large tiles: bf16 bmm
+    //     192 x 512 x 512 x 64, 64 x 128 32.8 us against 35.2 us on 256 x 256)
     if (desc->M > 1 && desc->N > 1) {
         const int64_t static_tiles =
             mfma ? ((p.M + pl.tile.bm - 1) / pl.tile.bm) * ((p.N + pl.tile.bn - 1) / pl.tile.bn) * p.batch : 0;
-        const bool plenty = static_tiles >= 2LL * dev_info().cus;
+        const bool plenty = static_tiles >= 2LL * dev_info().cus && p.K >= 1024;
         for (int i = 0; i < n && i < 32; ++i) {
             const MfmaTile &t = list[i];
             if (thin_tile(t) || t.sched == 2) continue;

@@ -443,6 +443,11 @@ def test_tile_candidates_skip_small_tiles_on_large_products():
     a2, b2 = torch.empty(2048, 4096, dtype=torch.bfloat16), torch.empty(4096, 2048, dtype=torch.bfloat16)
     cands = _lib.tile_candidates(_desc(torch.bfloat16, a2, b2), 24)
     assert any(c[:2] == (64, 64) for c in cands) and any(c[:2] == (32, 32) for c in cands), cands
+    # a short K keeps the small tiles (chained batch entries on them can win): bmm 192 x 512 x
+    # 512 x 64
+    a3, b3 = torch.empty(192, 512, 64, dtype=torch.bfloat16), torch.empty(192, 64, 512, dtype=torch.bfloat16)
+    cands = _lib.tile_candidates(_desc(torch.bfloat16, a3, b3), 24)
+    assert any(c[:2] == (64, 128) for c in cands), cands
 
 
 # ---- Python layer: layouts, scalars, errors (metalblas/dispatch.py) ---------------------------
