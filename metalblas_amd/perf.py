@@ -11,6 +11,7 @@ this GPU instead of wall clocks around ``torch.mps.synchronize``.
     python -m metalblas_amd.perf --report                # write profiles/shape_sweep_<gpu>.md
     python -m metalblas_amd.perf --bmm --check           # the bmm groups (bench/bench_bmm.py)
     python -m metalblas_amd.perf --trace-summary run_kernel_trace.csv --last 20
+    python -m metalblas_amd.perf --candidates 192x512x512x64   # what the autotuner times
 
 Numbers are best-of-``trials`` means over ``iters`` back-to-back calls, so a
 power-limited product reports its sustained rate, not its first call.
@@ -330,6 +331,50 @@ def run_group(name, shapes, dtype, layout=None, check=False, cool=0.0, out=print
     return rows, speedups
 
 
+def candidates(B, M, N, K, dtype=torch.bfloat16, out=print):
+    """Time the static plan and every autotune candidate (``mb_tile_candidates``) of one
+    row-major product (B > 1: batched), round-robin best-of as the tuner times them, beside
+    ``torch.bmm`` / ``torch.matmul``: what the one-shot tuner chooses between for this shape."""
+    import ctypes
+
+    from . import _lib, planner
+    g = torch.Generator(device="cuda").manual_seed(0)
+    a = _rand((B, M, K), dtype, g)
+    b = _rand((B, K, N), dtype, g)
+    c = torch.empty(B, M, N, dtype=dtype, device="cuda")
+    d = _lib.make_desc(dtype, B, M, N, K, (a, K, 1, M * K), (b, N, 1, K * N), (c, N, 1, M * N))
+    cands = _lib.tile_candidates(d, 24)
+    lib = _lib.load()
+    fns = [(lambda: torch.bmm(a, b)) if B > 1 else (lambda: torch.matmul(a[0], b[0]))]
+    labels = ["torch.bmm" if B > 1 else "torch.matmul"]
+    keep = []
+    for i, ch in enumerate(cands):
+        dd = _lib.MbGemmDesc.from_buffer_copy(d)
+        if i > 0:
+            planner.apply(dd, ch)
+        info = _lib.plan(dd)
+        nb = _lib.workspace_bytes(dd)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+        keep.append(ws)
+        dd.workspace = ctypes.c_void_p(ws.data_ptr())
+        dd.workspace_bytes = nb
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def fn(dd=dd):
+            _lib.check(lib.mb_gemm(ctypes.byref(dd), ctypes.c_void_p(stream)))
+        fns.append(fn)
+        tile = tuple(info.tile[:2])
+        sched = ("interleaved", "ping-pong", "deep-K")[info.tile[5] - 1] if info.tile[5] > 0 else "-"
+        labels.append(f"{'static plan' if i == 0 else 'candidate'} {tile[0]} x {tile[1]} "
+                      f"({info.tile[3]} x {info.tile[4]} waves, {sched}), {info.split_k} K slice(s), "
+                      f"grid {tuple(info.grid)}")
+    times = planner._fastest(fns, 5, 20, 7)
+    flops = 2.0 * B * M * N * K
+    out(f"=== candidates  {B} x {M} x {N} x {K}  dtype={str(dtype).replace('torch.', '')} ===")
+    for t, lab in sorted(zip(times, labels)):
+        out(f"  {t * 1e3:9.2f} us  {flops / t / 1e9:8.1f} TFLOP/s  {lab}")
+
+
 def machine_info():
     p = torch.cuda.get_device_properties(0)
     return {"gpu": torch.cuda.get_device_name(0), "arch": getattr(p, "gcnArchName", "?"),
@@ -385,6 +430,8 @@ def main(argv=None):
     p.add_argument("--report", action="store_true", help="write profiles/shape_sweep_<gpu>.md (bf16)")
     p.add_argument("--bmm", action="store_true", help="the bmm shape groups instead of the matmul ones")
     p.add_argument("--shape", metavar="MxNxK", help="one shape instead of the groups (with --layout: each layout)")
+    p.add_argument("--candidates", metavar="BxMxNxK", action="append",
+                   help="time the static plan and every autotune candidate of this row-major product")
     p.add_argument("--trace-summary", metavar="CSV", help="summarise a rocprofv3 kernel trace and exit")
     p.add_argument("--last", type=int, default=0, help="with --trace-summary: each kernel's last N dispatches")
     p.add_argument("--kernel", action="append", help="with --trace-summary / --pmc-summary: kernels whose name contains this")
@@ -416,6 +463,14 @@ def main(argv=None):
         return
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.last, args.kernel))
+        return
+    if args.candidates:
+        for spec in args.candidates:
+            shape = tuple(int(v) for v in spec.lower().split("x"))
+            if len(shape) != 4:
+                p.error("--candidates takes BxMxNxK")
+            for dt in (list(DTYPES.values()) if args.dtype == "all" else [DTYPES[args.dtype]]):
+                candidates(*shape, dtype=dt)
         return
     layouts = None
     if args.layout:
