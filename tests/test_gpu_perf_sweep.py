@@ -19,3 +19,12 @@ def test_sweep_layouts_check(capsys):
     out = capsys.readouterr().out
     assert "FAILED" not in out and "XX" not in out, out
     assert out.count("  ok") == len(perf.SHAPES["gemv"]) * len(perf.LAYOUTS)
+
+
+@pytest.mark.gpu
+def test_candidates_report(capsys):
+    """``--candidates`` times the static plan, every autotune rival and torch on one product."""
+    from metalblas_amd import perf
+    perf.main(["--candidates", "8x256x256x64"])
+    out = capsys.readouterr().out
+    assert "static plan" in out and "torch.bmm" in out and out.count("candidate ") >= 2, out
