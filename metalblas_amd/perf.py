@@ -364,7 +364,7 @@ def candidates(B, M, N, K, dtype=torch.bfloat16, out=print):
             _lib.check(lib.mb_gemm(ctypes.byref(dd), ctypes.c_void_p(stream)))
         fns.append(fn)
         tile = tuple(info.tile[:2])
-        sched = ("interleaved", "ping-pong", "deep-K")[info.tile[5] - 1] if info.tile[5] > 0 else "-"
+        sched = {1: "interleaved", 2: "ping-pong", 3: "deep-K"}.get(info.tile[5], f"schedule {info.tile[5] - 1}")
         labels.append(f"{'static plan' if i == 0 else 'candidate'} {tile[0]} x {tile[1]} "
                       f"({info.tile[3]} x {info.tile[4]} waves, {sched}), {info.split_k} K slice(s), "
                       f"grid {tuple(info.grid)}")
