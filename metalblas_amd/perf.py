@@ -13,6 +13,9 @@ this GPU instead of wall clocks around ``torch.mps.synchronize``.
     python -m metalblas_amd.perf --trace-summary run_kernel_trace.csv --last 20
     python -m metalblas_amd.perf --candidates 192x512x512x64   # what the autotuner times
 
+The ``torch`` column is ``torch.matmul``; for int8 it is ``torch._int_mm`` (int32 outputs),
+torch's only int8 product on the GPU.
+
 Numbers are best-of-``trials`` means over ``iters`` back-to-back calls, so a
 power-limited product reports its sustained rate, not its first call.
 
@@ -149,6 +152,10 @@ def bench_one(M, N, K, dtype, build_a=_rm, build_b=_rm, check=False, cool=0.0):
     t_torch = None
     if dtype not in (torch.complex32,) and (dtype.is_floating_point or dtype.is_complex):
         t_torch = _time(lambda: torch.matmul(a, b), iters, 5, 3)
+    elif dtype == torch.int8 and M > 16 and K % 8 == 0 and N % 8 == 0:
+        # torch has no int8 matmul on the GPU; its library product is torch._int_mm (hipBLASLt),
+        # which writes int32 outputs (4x the output bytes of the wrapping int8 result)
+        t_torch = _time(lambda: torch._int_mm(a, b), iters, 5, 3)
     t_mb = _time(lambda: _mb.matmul(a, b), iters, 5, 3)
     if cool > 0:
         time.sleep(cool * (time.perf_counter() - t0))
@@ -315,6 +322,8 @@ def run_group(name, shapes, dtype, layout=None, check=False, cool=0.0, out=print
     build_a, build_b = LAYOUTS[layout or "rm_rm"]
     rows, speedups = [], []
     out(f"\n=== {name}  dtype={str(dtype).replace('torch.', '')}" + (f"  layout={layout}" if layout else "") + " ===")
+    if dtype == torch.int8:
+        out("(torch column: torch._int_mm, int8 x int8 -> int32; mb: int8 result)")
     out(HEADER + ("  chk" if check else ""))
     for (M, N, K) in shapes:
         try:

@@ -28,3 +28,13 @@ def test_candidates_report(capsys):
     perf.main(["--candidates", "8x256x256x64"])
     out = capsys.readouterr().out
     assert "static plan" in out and "torch.bmm" in out and out.count("candidate ") >= 2, out
+
+
+@pytest.mark.gpu
+def test_int8_rows_time_int_mm(capsys):
+    """int8 rows time torch._int_mm (hipBLASLt, int32 outputs) beside the library's int8 product."""
+    from metalblas_amd import perf
+    perf.main(["--shape", "512x512x512", "--dtype", "i8", "--check"])
+    out = capsys.readouterr().out
+    assert "torch._int_mm" in out and "  ok" in out and "FAILED" not in out, out
+    assert "median speedup" in out, out
