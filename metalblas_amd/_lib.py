@@ -256,11 +256,18 @@ _WS_LOCK = threading.Lock()
 
 def workspace(idx: int, stream: int, nbytes: int):
     """(tensor, lock): a device tensor of at least ``nbytes`` of scratch for work queued on
-    ``stream``, and the lock to hold while queuing the kernels that use it.
+    ``stream`` (torch's current stream), and the lock to hold while queuing the kernels that use
+    it.
 
     The caller keeps the tensor referenced until its launch is queued: another host thread that
     needs more scratch on the same stream replaces the kept tensor, and the reference keeps the
-    old block out of the caching allocator until then (stream order protects it after)."""
+    old block out of the caching allocator until then (stream order protects it after).
+
+    While the stream is being captured into a HIP graph, the scratch is a new tensor instead:
+    torch allocates it from the graph's private pool, which the graph holds for its replays.  A
+    kept tensor could be replaced and freed by a later call while the graph still uses it."""
+    if torch._C._cuda_isCurrentStreamCapturing():
+        return torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", idx)), _NO_LOCK
     key = (idx, stream)
     with _WS_LOCK:
         ent = _WS.get(key)

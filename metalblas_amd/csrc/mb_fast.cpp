@@ -142,10 +142,14 @@ bool launch_cached(int dt, int64_t batch, int64_t M, int64_t N, int64_t K, const
     d.c.ptr = c.data_ptr();
     const int dev = c.get_device();
     hipStream_t st = c10::hip::getCurrentHIPStream(dev).stream();
-    at::Tensor once;   // a per-call workspace above kWsKeep: freed after the launch is queued
+    at::Tensor once;   // a per-call workspace: freed after the launch is queued
     const int64_t ws_bytes = it->second.ws_bytes;
     if (ws_bytes > 0) {
-        if (ws_bytes <= kWsKeep) {
+        // under HIP graph capture the per-call tensor comes from the graph's private pool, which
+        // the graph holds for its replays; the kept one could be replaced and freed meanwhile
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+        if (ws_bytes <= kWsKeep && cap == hipStreamCaptureStatusNone) {
             at::Tensor &ws = g_ws[WsKey{dev, (void *)st}];
             if (!ws.defined() || ws.numel() < ws_bytes)
                 ws = at::empty({std::max<int64_t>(ws_bytes, int64_t(1) << 20)}, c.options().dtype(at::kByte));

@@ -144,20 +144,25 @@ def _launch(dtype, batch, M, N, K, a, b, out, *, bias=None, epilogue=None, conj_
            bias.stride() if bias is not None else None, pbias & 255, conj_a, conj_b, epilogue, backend,
            tile if tile is None else tuple(tile), swizzle_log, idx, _planner.enabled())
     hit = _DESC_CACHE.get(key)
+    keep = True
     if hit is None:
         desc = _lib.make_desc(dtype, batch, M, N, K, _mat(a), _mat(b), _mat(out),
                               _mat(bias) if bias is not None else None,
                               conj_a=conj_a, conj_b=conj_b, epilogue=epilogue, backend=backend,
                               tile=tile, swizzle_log=swizzle_log)
-        if backend == _lib.BACKEND_AUTO and tile is None:
+        # under HIP graph capture the tuner cannot time candidates (it synchronises): the static
+        # plan is captured and not kept, so the first eager call of the signature still tunes
+        keep = not torch._C._cuda_isCurrentStreamCapturing()
+        if backend == _lib.BACKEND_AUTO and tile is None and keep:
             with torch.cuda.device(idx):
                 _planner.tune(desc, a, b, out, bias)
         hit = (desc, _lib.workspace_bytes(desc))
-        if len(_DESC_CACHE) >= _DESC_CACHE_CAP:
-            clear_descriptors()
-        _DESC_CACHE[key] = hit
+        if keep:
+            if len(_DESC_CACHE) >= _DESC_CACHE_CAP:
+                clear_descriptors()
+            _DESC_CACHE[key] = hit
     template, ws_bytes = hit
-    if (_FAST is not None and bias is None and epilogue is None and not conj_a and not conj_b
+    if (keep and _FAST is not None and bias is None and epilogue is None and not conj_a and not conj_b
             and backend == _lib.BACKEND_AUTO and tile is None and swizzle_log is None):
         _FAST.register(a, b, out, bytes(template), ws_bytes)   # later calls take the fast path
     desc, w, ref = _thread_desc(key, template)

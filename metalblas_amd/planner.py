@@ -156,6 +156,8 @@ def tune(desc, a, b, out, bias=None) -> None:
         return
     if desc.batch * desc.M * desc.N * desc.K < _MIN_WORK:
         return
+    if torch._C._cuda_isCurrentStreamCapturing():   # timing synchronises: not under graph capture
+        return
     _load_cache()
     device = out.device
     key = _key(desc, device)
