@@ -580,6 +580,23 @@ def test_autotune_switch(monkeypatch):
     assert planner.enabled()
 
 
+def test_tuner_skips_under_graph_capture(monkeypatch):
+    """Timing candidates synchronises, which a HIP graph capture forbids: under capture the
+    tuner leaves the descriptor's request alone and records nothing."""
+    monkeypatch.delenv("METALBLAS_AUTOTUNE", raising=False)
+    monkeypatch.setattr(torch._C, "_cuda_isCurrentStreamCapturing", lambda: True)
+    planner.clear()
+    d = _lib.make_desc(torch.bfloat16, 1, 4096, 4096, 4096, (None, 4096, 1, 0), (None, 4096, 1, 0),
+                       (None, 4096, 1, 0))
+    before = bytes(d)
+
+    class Unused:
+        def __getattr__(self, name):
+            raise AssertionError(f"the tuner touched its output ({name}) under capture")
+    planner.tune(d, None, None, Unused())
+    assert bytes(d) == before and planner.cached() == {}
+
+
 def test_tuner_scratch_keeps_output_layout():
     """Candidates are timed into scratch with the real output's strides and pointer alignment."""
     base = torch.empty(40 * 33 + 17, dtype=torch.bfloat16)
