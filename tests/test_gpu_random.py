@@ -1,6 +1,7 @@
 """Seeded random products against the CPU oracle: combinations of dtype, shape, batch, operand
 layout (transposed, row-sliced, storage offset, stride-0 batch), fused epilogue and tile request
-that the hand-picked cases of test_gpu_parity.py do not pair up.  The case list is a fixed
+that the hand-picked cases of test_gpu_parity.py do not pair up, and output views written
+through out= (column-major, row-sliced, misaligned).  The case list is a fixed
 function of the seed, so a failure names a reproducible case.  Mirrors the reference's
 randomised coverage matrix (tests/test_basic.py:166-255) at sizes the oracle finishes quickly.
 """
@@ -81,3 +82,73 @@ def test_random_products(dev, case):
     else:
         got = mb.matmul(_to(a, dev), bd)
     assert_parity(got, a, b, tag=tag)
+
+
+# ---- output layouts (out=): column-major, row-sliced and misaligned outputs, with sentinels in
+# the gaps of the output buffer, which no product may write
+
+OUT_LAYOUTS = ["t", "rows", "offset"]
+
+
+def _out_cases(n, seed):
+    rng = random.Random(seed)
+    cases = []
+    for i in range(n):
+        dtype = rng.choice(DTYPES)
+        batch = rng.choice([0, 0, 2, 5])
+        M, N, K = (rng.choice([1, 7, 64, 100, 129, 256, 300]) for _ in range(3))
+        cases.append((i, dtype, batch, M, N, K, rng.choice(OUT_LAYOUTS), rng.random() < 0.3))
+    return cases
+
+
+def _sentinel(dtype):
+    if dtype in INTS:
+        return 77
+    return complex(float("nan"), 0) if dtype in COMPLEX else float("nan")
+
+
+def _out_buffer(shape, dtype, dev, layout):
+    """(out view, the whole buffer, a mask of the buffer's elements outside the view)."""
+    *bs, r, c = shape
+    if layout == "t":
+        buf = torch.full((*bs, c, r), _sentinel(dtype), dtype=dtype, device=dev)
+        return buf.transpose(-2, -1), buf, torch.zeros(buf.shape, dtype=torch.bool)
+    if layout == "rows":
+        buf = torch.full((*bs, 2 * r, c), _sentinel(dtype), dtype=dtype, device=dev)
+        gap = torch.zeros(buf.shape, dtype=torch.bool)
+        gap[..., 1::2, :] = True
+        return buf[..., ::2, :], buf, gap
+    n = (bs[0] if bs else 1) * r * c
+    buf = torch.full((5 + n + 3,), _sentinel(dtype), dtype=dtype, device=dev)
+    gap = torch.ones(buf.shape, dtype=torch.bool)
+    gap[5:5 + n] = False
+    return buf[5:5 + n].view(*bs, r, c), buf, gap
+
+
+def _untouched(buf, gap, dtype):
+    v = buf.cpu()[gap]
+    if dtype in INTS:
+        return bool((v == 77).all())
+    return bool(torch.isnan(v.real if dtype in COMPLEX else v.float()).all())
+
+
+@pytest.mark.parametrize("case", _out_cases(96, 2027), ids=lambda c: f"o{c[0]}")
+def test_random_output_layouts(dev, case):
+    i, dtype, batch, M, N, K, layout, epi = case
+    g = gen(5000 + i)
+    bsh = (batch,) if batch else ()
+    a, b = rand((*bsh, M, K), dtype, g), rand((*bsh, K, N), dtype, g)
+    out, buf, gap = _out_buffer((*bsh, M, N), dtype, dev, layout)
+    tag = f"output layout case {case}"
+    if epi:
+        beta, alpha = (2, 3) if dtype in INTS else ((0.5 - 1j, 2.0) if dtype in COMPLEX else (0.5, 2.0))
+        bias = rand((N,), dtype, g)
+        op = mb.baddbmm if batch else mb.addmm
+        got = op(bias.to(dev), a.to(dev), b.to(dev), beta=beta, alpha=alpha, out=out)
+        assert got is out
+        assert_parity(out, a, b, bias=bias, beta=beta, alpha=alpha, tag=tag)
+    else:
+        got = (mb.bmm if batch else mb.matmul)(a.to(dev), b.to(dev), out=out)
+        assert got is out
+        assert_parity(out, a, b, tag=tag)
+    assert _untouched(buf, gap, dtype), f"{tag}: a product wrote outside its output view"
