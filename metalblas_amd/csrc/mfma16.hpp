@@ -533,10 +533,26 @@ __device__ __forceinline__ void store_tile16(const GemmArgs &g, typename AccT<T,
 // products with a short K (where the output dominates the traffic) to about 2.5 TB/s of writes.
 // Taken for row-major outputs with 16-byte aligned rows and no split-K planes; a fused epilogue
 // is applied in registers before the tile is staged.
-template <class T, int BM, int BN> struct CStage {
+// Bank layout (64 banks of 4 bytes).  The 16 x 16 blocks (MS = 16) and 8-bit tiles write 16 rows
+// per 16-lane group and use a 16-byte row pad.  The 32 x 32 blocks of 16-bit tiles write 32 rows
+// of one 8-byte column piece per half-wave, which no 16-byte-granular pitch spreads over the
+// banks, and the pad makes each 16-lane group of the row-wise reads straddle two rows' banks: their
+// rows are unpadded, and the 8-byte pieces of row r sit at byte column c ^ xor_bytes(r), a
+// permutation of the row's pieces (within each 256-byte window) that gives the 32 rows of a
+// half-wave distinct banks (64-wide rows alternate bank halves, so row pairs share the XOR).
+template <class T, int BM, int BN, int MS> struct CStage {
     static_assert(sizeof(T) <= 2, "the staged store packs 4 outputs into 8 or 4 bytes");
-    static constexpr int PITCH = BN * (int)sizeof(T) + 16;
+    static constexpr bool SWZ = sizeof(T) == 2 && MS == 32 && BN >= 64;
+    static constexpr int PITCH = SWZ ? BN * 2 : BN * (int)sizeof(T) + 16;
     static constexpr int BYTES = BM * PITCH;
+    __device__ __forceinline__ static int xor_bytes(int row) {
+        if constexpr (!SWZ)
+            return 0;
+        else if constexpr (BN == 64)
+            return 8 * ((row >> 1) & 15);
+        else
+            return 8 * (row & 31);
+    }
 };
 
 template <class T> __device__ __forceinline__ bool staged_store_ok(const GemmArgs &g) {
@@ -547,7 +563,7 @@ template <class T> __device__ __forceinline__ bool staged_store_ok(const GemmArg
 // this wave's accumulators (the block layout of store_tile16) into the staged tile; mw / nw are
 // tile-relative and m0 / n0 the tile's origin in C.  A fused epilogue (alpha, beta and the bias
 // read at the output's coordinates) is applied before the one rounding, as store_tile16 does.
-template <class T, int TM, int TN, int MS, int PITCH>
+template <class T, int TM, int TN, int MS, class CS>
 __device__ __forceinline__ void stage_acc(const GemmArgs &g, char *ct, typename AccT<T, MS>::type (&acc)[TN][TM],
                                           int mw, int nw, int m0, int n0, int bz, int lane) {
     constexpr int NQ = MS * MS / 256;
@@ -586,7 +602,7 @@ __device__ __forceinline__ void stage_acc(const GemmArgs &g, char *ct, typename 
                     for (int r = 0; r < 4; ++r)
                         o[r] = Tr<T>::down(epi_apply<T>((A)acc[i][j][4 * q + r], bv + r, g.s, g.beta_nz, g.alpha_nz));
                 }
-                char *dst = ct + row * PITCH + col * (int)sizeof(T);
+                char *dst = ct + row * CS::PITCH + ((col * (int)sizeof(T)) ^ CS::xor_bytes(row));
                 if constexpr (sizeof(T) == 2) {
                     uint2 u;
                     __builtin_memcpy(&u, o, 8);
@@ -614,9 +630,9 @@ template <class T> __device__ __forceinline__ T chunk_elem(const uint4 &v, int k
 
 // the staged tile out to C rows m0.., columns n0.. (16 bytes per thread and step; the ragged
 // right edge element by element); STREAM: non-temporal stores (an output larger than the cache)
-template <class T, int BM, int BN, int NT, bool STREAM>
+template <class T, int BM, int BN, int MS, int NT, bool STREAM>
 __device__ __forceinline__ void store_staged(const GemmArgs &g, const char *ct, int m0, int n0, int bz, int tid) {
-    constexpr int PITCH = CStage<T, BM, BN>::PITCH;
+    using CS = CStage<T, BM, BN, MS>;
     constexpr int EPC = 16 / (int)sizeof(T);
     constexpr int CPR = BN / EPC;
     T *Cb = (T *)g.c + bz * g.c_bs;
@@ -624,7 +640,9 @@ __device__ __forceinline__ void store_staged(const GemmArgs &g, const char *ct, 
     for (int c = tid; c < rows * CPR; c += NT) {
         const int r = c / CPR, col = (c % CPR) * EPC;
         if (col >= cols) continue;
-        const uint4 v = *(const uint4 *)(ct + r * PITCH + col * (int)sizeof(T));
+        const int x = CS::xor_bytes(r);   // 16-byte chunk col, its 8-byte halves swapped when x & 8
+        uint4 v = *(const uint4 *)(ct + r * CS::PITCH + (((col * (int)sizeof(T)) ^ x) & ~15));
+        if (x & 8) v = make_uint4(v.z, v.w, v.x, v.y);
         T *dst = Cb + (int64_t)(m0 + r) * g.c_rs + n0 + col;
         if (col + EPC <= cols) {
             if constexpr (STREAM) {
@@ -655,7 +673,7 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
     // LDS read instructions per k-step (a transposing fragment takes two)
     constexpr int NREAD_RAW = TM * (A_KC ? 1 : 2) + TN * (B_KC ? 1 : 2);
     constexpr int NREAD = NREAD_RAW < TM * TN ? NREAD_RAW : TM * TN;
-    using CS = CStage<T, BM, BN>;
+    using CS = CStage<T, BM, BN, 32>;
     constexpr int SMEM = 2 * STAGE > CS::BYTES ? 2 * STAGE : CS::BYTES;
 
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -779,12 +797,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
             if (last) {
                 __syncthreads();   // every wave is done with this stage before it holds the output
                 if (staged_store_ok<T>(g)) {
-                    stage_acc<T, TM, TN, 32, CS::PITCH>(g, cur, acc, wm * WTM, wn * WTN, m0, n0, e, lane);
+                    stage_acc<T, TM, TN, 32, CS>(g, cur, acc, wm * WTM, wn * WTN, m0, n0, e, lane);
                     __syncthreads();
                     if (g.c_stream)
-                        store_staged<T, BM, BN, 64 * NW, true>(g, cur, m0, n0, e, tid);
+                        store_staged<T, BM, BN, 32, 64 * NW, true>(g, cur, m0, n0, e, tid);
                     else
-                        store_staged<T, BM, BN, 64 * NW, false>(g, cur, m0, n0, e, tid);
+                        store_staged<T, BM, BN, 32, 64 * NW, false>(g, cur, m0, n0, e, tid);
                 } else {
                     store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, e, ks, lane);
                 }
@@ -900,12 +918,12 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm16(GemmArgs g) {
 
         if (staged_store_ok<T>(g)) {
             __syncthreads();   // every wave is done with the operand stages
-            stage_acc<T, TM, TN, 32, CS::PITCH>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
+            stage_acc<T, TM, TN, 32, CS>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
             __syncthreads();
             if (g.c_stream)
-                store_staged<T, BM, BN, 64 * NW, true>(g, smem, m0, n0, bz, tid);
+                store_staged<T, BM, BN, 32, 64 * NW, true>(g, smem, m0, n0, bz, tid);
             else
-                store_staged<T, BM, BN, 64 * NW, false>(g, smem, m0, n0, bz, tid);
+                store_staged<T, BM, BN, 32, 64 * NW, false>(g, smem, m0, n0, bz, tid);
         } else {
             store_tile16<T, TM, TN>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         }
@@ -1124,7 +1142,7 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
     using TA = Tile16<BM, NW, A_KC, ES, MS>;
     using TB = Tile16<BN, NW, B_KC, ES, MS>;
     constexpr int STAGE = TA::BYTES + TB::BYTES;
-    using CS = CStage<T, BM, BN>;
+    using CS = CStage<T, BM, BN, MS>;
     constexpr int SMEM = 2 * STAGE > CS::BYTES ? 2 * STAGE : CS::BYTES;
 
     __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -1347,12 +1365,12 @@ __global__ __launch_bounds__(512) void k_gemm16pp(GemmArgs g) {
         }
         if (staged_store_ok<T>(g)) {
             __syncthreads();   // both wave groups are done with the operand stages
-            stage_acc<T, TM, TN, MS, CS::PITCH>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
+            stage_acc<T, TM, TN, MS, CS>(g, smem, acc, wm * WTM, wn * WTN, m0, n0, bz, lane);
             __syncthreads();
             if (g.c_stream)
-                store_staged<T, BM, BN, 512, true>(g, smem, m0, n0, bz, tid);
+                store_staged<T, BM, BN, MS, 512, true>(g, smem, m0, n0, bz, tid);
             else
-                store_staged<T, BM, BN, 512, false>(g, smem, m0, n0, bz, tid);
+                store_staged<T, BM, BN, MS, 512, false>(g, smem, m0, n0, bz, tid);
         } else {
             store_tile16<T, TM, TN, MS>(g, acc, m0 + wm * WTM, n0 + wn * WTN, bz, ks, lane);
         }
