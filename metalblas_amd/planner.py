@@ -29,6 +29,7 @@ import ctypes
 import json
 import os
 import threading
+import time
 
 import torch
 
@@ -118,12 +119,46 @@ def cached() -> dict:
     return dict(_PLANS)
 
 
+# GPU spin (torch.cuda._sleep cycles, which count shader clocks) queued ahead of each timed
+# batch: 1.5 x the host time the previous batch took to queue, at up to 3 GHz
+_HOLD = [1 << 20]
+_HOLD_MIN, _HOLD_MAX = 1 << 18, 1 << 28
+
+
+def _time_batch(fn, iters):
+    """GPU time per call (ms) of ``iters`` back-to-back calls of ``fn``.  A small product's
+    call costs more host time (Python, the launch) than GPU time, so events around calls queued
+    as the host issues them would time the host.  A spin kernel queued first keeps the GPU busy
+    while the calls are queued; if it ended before the last call was queued, the batch is timed
+    again behind a spin sized from the host time just measured."""
+    sleep = getattr(torch.cuda, "_sleep", None)
+    while True:
+        held = None
+        if sleep is not None:
+            sleep(_HOLD[0])
+            held = torch.cuda.Event()
+            held.record()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        host_us = (time.perf_counter() - t0) * 1e6
+        late = held is not None and held.query()
+        e.record()
+        e.synchronize()
+        grown = _HOLD[0] >= _HOLD_MAX
+        _HOLD[0] = min(_HOLD_MAX, max(_HOLD_MIN, int(host_us * 1.5 * 3000)))
+        if not late or grown:
+            return s.elapsed_time(e) / iters
+
+
 def _fastest(fns, warmup, iters, reps):
     """Per-call times (ms, best of ``reps``) of ``fns``, as the reference's ``_fastest``
     (metalblas/float_dispatch.py:419-433): every candidate's warmup first, then the timed
     repetitions round-robin over the candidates, so a clock that is still ramping up (the
     first call of a shape often comes to an idle GPU) does not favour the candidates timed
-    last."""
+    last.  Each repetition times GPU work only (``_time_batch``)."""
     for fn in fns:
         for _ in range(warmup):
             fn()
@@ -131,13 +166,7 @@ def _fastest(fns, warmup, iters, reps):
     times = [float("inf")] * len(fns)
     for _ in range(reps):
         for i, fn in enumerate(fns):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record()
-            for _ in range(iters):
-                fn()
-            e.record()
-            e.synchronize()
-            times[i] = min(times[i], s.elapsed_time(e) / iters)
+            times[i] = min(times[i], _time_batch(fn, iters))
     return times
 
 

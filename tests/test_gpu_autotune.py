@@ -164,3 +164,22 @@ def test_cross_family_candidates_and_tuned_plan_match_oracle(dev, monkeypatch, c
     assert torch.equal(again, got)
     planner.clear()
     dispatch.clear_descriptors()
+
+
+def test_tuner_times_gpu_work_not_host_time(dev):
+    """A candidate whose calls cost far more host time than GPU time is timed by its GPU work:
+    each call here spends 200 us on the host before queuing a ~10 us product."""
+    import time
+    a = rand((256, 256), torch.bfloat16, gen(3)).to(dev)
+    b = rand((256, 256), torch.bfloat16, gen(4)).to(dev)
+
+    def slow_host():
+        t = time.perf_counter()
+        while time.perf_counter() - t < 2e-4:
+            pass
+        mb.matmul(a, b)
+    for _ in range(3):
+        slow_host()
+    torch.cuda.synchronize()
+    ms = planner._time_batch(slow_host, 10)
+    assert ms < 0.1, f"timed {ms * 1e3:.1f} us per call: host time leaked into the GPU timing"
