@@ -58,13 +58,13 @@ TRAFFIC = {
     "bf16_2048x4096x2048_col_sliced": 1.0938e+08,
     "bf16_2048x4096x2048_offset17": 1.0938e+08,
     "bf16_2048x4096x2048_addmm": 1.0941e+08,
-    "f16_bmm_8x512x512x256": 2.3209e+07,            # k_gemm16 (the tile the tuner took: 64 x 64)
-    "f16_bmm_broadcastB": 9.6553e+06,               # k_gemm16 128 x 64
+    "f16_bmm_8x512x512x256": 2.3314e+07,            # k_gemm16 (the tile the tuner took: 128 x 64)
+    "f16_bmm_broadcastB": 9.6800e+06,               # k_gemm16 128 x 64
     "f16_splitk_128x128x65536": 3.7852e+07,         # the deep-K k_thin16 64 x 64
-    "c64_gemm_2048_conjA": 3.7532e+08,              # k_gemm_mfma<float> after k_cplx_expand
+    "c64_gemm_2048_conjA": 3.7610e+08,              # k_gemm_mfma<float> after k_cplx_expand
     "c64_gemv_8192": 5.3758e+08,                    # k_cdot_wg
-    "i8_gemm_4096": 1.1794e+08,                     # k_gemm16pp<int8, ...>
-    "i32_gemm_256": 3.0065e+06,                     # k_gemm_generic<int32, 16>
+    "i8_gemm_4096": 1.1798e+08,                     # k_gemm16pp<int8, ...>
+    "i32_gemm_256": 2.9991e+06,                     # k_gemm_generic<int32, 16>
 }
 
 
