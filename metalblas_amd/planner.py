@@ -130,9 +130,9 @@ def _time_batch(fn, iters):
     call costs more host time (Python, the launch) than GPU time, so events around calls queued
     as the host issues them would time the host.  A spin kernel queued first keeps the GPU busy
     while the calls are queued; if it ended before the last call was queued, the batch is timed
-    again behind a spin sized from the host time just measured."""
+    again (up to four times in all) behind a spin sized from the host time just measured."""
     sleep = getattr(torch.cuda, "_sleep", None)
-    while True:
+    for attempt in range(4):
         held = None
         if sleep is not None:
             sleep(_HOLD[0])
@@ -149,7 +149,7 @@ def _time_batch(fn, iters):
         e.synchronize()
         grown = _HOLD[0] >= _HOLD_MAX
         _HOLD[0] = min(_HOLD_MAX, max(_HOLD_MIN, int(host_us * 1.5 * 3000)))
-        if not late or grown:
+        if not late or grown or attempt == 3:
             return s.elapsed_time(e) / iters
 
 
