@@ -157,7 +157,7 @@ int mb_gemm(const mb_gemm_desc *desc, void *stream);
  * it is for callers that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The split-K planes, operand copies and complex
  * expansions a product needs run in a static per-device buffer of
- * mb_gemm_noalloc_scratch_bytes() bytes (64 MiB, enough for every BASELINE workload) that the
+ * mb_gemm_noalloc_scratch_bytes() bytes (64 MiB, enough for every benchmark workload) that the
  * library holds on each device it runs on until the process ends; desc->workspace and
  * desc->workspace_bytes are ignored.  The plan is the one mb_gemm() runs with a workspace of
  * mb_gemm_noalloc_scratch_bytes() bytes: the same kernels, hence identical results, for every

@@ -170,7 +170,7 @@ def check_values(got, c_ref, exact, dtype, K, scale=1.0, tag="", strict=False):
     assert ref_err <= ref_lim, f"{tag}: reference limit {ref_err:.3e} > {ref_lim:.3e}"
 
 
-# ---- whole outputs of the BASELINE workloads ----------------------------------------------------
+# ---- whole outputs of the benchmark workloads ---------------------------------------------------
 
 def spread_rows(M, count, salt=53):
     """``count`` rows spread over [0, M): the first and last rows plus one row per equal band,

@@ -18,7 +18,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _cases(dev):
-    """(tag, call, check-args): the BASELINE shapes the reference tunes, plus a complex64
+    """(tag, call, check-args): the benchmark shapes the reference tunes, plus a complex64
     product (its four real products are tuned through the float GEMM in the reference)."""
     g = gen(21)
     a = torch.randn(2048, 4096, generator=g).to(torch.bfloat16).to(dev)

@@ -1,4 +1,4 @@
-"""GPU parity at every BASELINE workload, through the exact calls bench.py times.
+"""GPU parity at every benchmark workload, through the exact calls bench.py times.
 
 Each case builds bench.py's workload group (the same seeds, shapes, operand layouts, ``out=``
 buffers and API entry points), runs the benched call once, and checks the output with

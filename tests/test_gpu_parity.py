@@ -475,7 +475,7 @@ def test_thin_rows_batched_and_short_k(dev, dtype, case, a_layout):
 
 @pytest.mark.parametrize("n", [8192, 16384])
 def test_gemv_config2_sizes(dev, n):
-    """BASELINE config 2 at full size: y = W @ x, x @ W and 8-vector thin products,
+    """Benchmark config 2 at full size: y = W @ x, x @ W and 8-vector thin products,
     checked on sampled rows against the oracle."""
     g = gen(1)
     W = torch.randn(n, n, generator=g).to(torch.bfloat16)
@@ -558,7 +558,7 @@ def test_unaligned_operands(dev, dtype, case):
 
 
 def test_unaligned_addmm_config3_offset(dev):
-    """BASELINE config 3 'offset' layout: a contiguous view at storage offset 17, with addmm."""
+    """Benchmark config 3 'offset' layout: a contiguous view at storage offset 17, with addmm."""
     g = gen(3)
     M, K, N = 1024, 2048, 768
     flat = rand((17 + M * K,), torch.bfloat16, g)

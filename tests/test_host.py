@@ -1,5 +1,5 @@
 """CPU tests of the host side: the C ABI's exports and struct layout, the planner's decisions
-for the BASELINE configurations, error mapping, and the Python layout/scalar logic of
+for the benchmark configurations, error mapping, and the Python layout/scalar logic of
 metalblas/dispatch.py that the drop-in keeps.  Nothing here launches a kernel."""
 import ctypes
 import json
@@ -149,7 +149,7 @@ def test_abi_rejects_bad_descriptors_before_launch():
     assert lib.mb_tile_candidates(ctypes.byref(d), tiles, 8) == _lib.ERR_INVALID_ARG
 
 
-# ---- planner decisions at the BASELINE configurations (256 CUs assumed without a GPU) ---------
+# ---- planner decisions at the benchmark configurations (256 CUs assumed without a GPU) ---------
 
 def test_plan_config3_square_bf16_uses_matrix_cores():
     a = torch.empty(8192, 8192, dtype=torch.bfloat16)
@@ -469,7 +469,7 @@ def test_tile_candidates_are_compiled_tiles(dt):
 
 
 def test_unit_lead_classification():
-    """metalblas/dispatch.py:23-35 on the BASELINE config-3 layouts."""
+    """metalblas/dispatch.py:23-35 on the benchmark's config-3 layouts."""
     M, K = 64, 96
     rm = torch.empty(M, K)
     assert dispatch._unit_lead(rm, M, K) == (False, K)
