@@ -38,11 +38,13 @@ def _to(t, dev):
     return base.to(dev).as_strided(t.shape, t.stride(), t.storage_offset())
 
 
-def _cases(n, seed):
+def _cases(n, seed, dtypes=None):
+    """n seeded cases; with ``dtypes`` (the dtypes the first list leaves out) the case indices
+    start at 1000."""
     rng = random.Random(seed)
     cases = []
-    for i in range(n):
-        dtype = rng.choice(DTYPES)
+    for i in range(1000 if dtypes else 0, (1000 if dtypes else 0) + n):
+        dtype = rng.choice(dtypes or DTYPES)
         batch = rng.choice([0, 0, 1, 3, 8])             # 0: a 2-D product
         M, N, K = (rng.choice([1, 7, 33, 64, 100, 128, 200, 257, 320]) for _ in range(3))
         if rng.random() < 0.2:                          # a short K over many batch entries
@@ -55,7 +57,11 @@ def _cases(n, seed):
     return cases
 
 
-@pytest.mark.parametrize("case", _cases(256, 2026), ids=lambda c: f"r{c[0]}")
+MORE_DTYPES = [torch.int16, torch.int64, torch.complex32, torch.float32, torch.uint8]
+
+
+@pytest.mark.parametrize("case", _cases(256, 2026) + _cases(64, 2028, MORE_DTYPES),
+                         ids=lambda c: f"r{c[0]}" if c[0] < 1000 else f"m{c[0] - 1000}")
 def test_random_products(dev, case):
     i, dtype, batch, M, N, K, la, lb, epi, tile = case
     g = gen(1000 + i)
